@@ -1,0 +1,483 @@
+// Block-sparse flash-attention forward for LVSA on gfx950 (MI355X).
+//
+// Work unit: one query tile of BM = 128 rows of one head (4 waves x 32 rows)
+// walks the key blocks (BN = 64 rows each) listed for it by the block plan.
+//
+//   S^T = K · Q^T      v_mfma_f32_32x32x16_{bf16,f16}: A = K rows from LDS
+//                      (ds_read_b128), B = Q held in registers for the tile
+//   softmax            every lane owns one query row (column of S^T): 16 of
+//                      the 32 keys of a 32-key sub-tile, the other 16 sit in
+//                      lane ^ 32; the running max uses a lazy rescale (O and
+//                      the row sum are rescaled only when the block maximum
+//                      exceeds the running one by more than 2^8)
+//   O^T += V^T · P^T   A = V^T read from the row-major LDS tile with
+//                      ds_read_b64_tr_b16, B = P (bf16/f16) straight from the
+//                      S^T accumulator registers (key order permuted
+//                      identically on both operands)
+//
+// K and V tiles are DMA'd global -> LDS (global_load_lds_dwordx4) into a
+// double buffer, with a 16-byte-chunk XOR swizzle that keeps both the K reads
+// and the transposing V reads free of bank conflicts.  The LDS image of a
+// tile is row-major, so K and V are read in place from the caller's
+// [B, S, H, D] tensors: no gather, no transpose, no padding copies.
+#include "lvsa_common.h"
+
+namespace lvsa {
+namespace {
+
+constexpr int kBM = 128;
+constexpr int kBN = 64;
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kXcds = 8;
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef short shortx4 __attribute__((ext_vector_type(4)));
+typedef short shortx8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) char lds_char;
+
+struct AttnParams {
+  const char* q;
+  const char* k;
+  const char* v;
+  const char* kx;
+  const char* vx;
+  const char* qt;
+  char* o;
+  char* ot;
+  float* lse;
+  float* lse_t;
+  int64_t q_str[3], k_str[3], v_str[3], kx_str[3], vx_str[3], qt_str[3], o_str[3], ot_str[3];
+  int B, H, Hkv, group;
+  int n_q, n_k, n_x, n_tq;
+  float scale_log2;
+  const int32_t* tile_indptr;
+  const uint2* entries;
+  int n_tiles, n_vt, n_tt;
+  const uint32_t* rel;
+  int words, R, C, q_frame0;
+  int64_t q_tok0, k_tok0;
+  int total_work;
+};
+
+template <typename E>
+struct Ops;
+
+template <>
+struct Ops<__bf16> {
+  typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+  typedef __bf16 v2 __attribute__((ext_vector_type(2)));
+  __device__ static floatx16 mfma(v8 a, v8 b, floatx16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  __device__ static v2 pack(float a, float b) { return v2{(__bf16)a, (__bf16)b}; }
+  __device__ static float dot2(v2 a, float acc) {
+    const v2 one = {(__bf16)1.0f, (__bf16)1.0f};
+    return __builtin_amdgcn_fdot2_f32_bf16(a, one, acc, false);
+  }
+  __device__ static unsigned short bits(float x) { return __builtin_bit_cast(unsigned short, (__bf16)x); }
+};
+
+template <>
+struct Ops<_Float16> {
+  typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+  typedef _Float16 v2 __attribute__((ext_vector_type(2)));
+  __device__ static floatx16 mfma(v8 a, v8 b, floatx16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  __device__ static v2 pack(float a, float b) { return v2{(_Float16)a, (_Float16)b}; }
+  __device__ static float dot2(v2 a, float acc) {
+    const v2 one = {(_Float16)1.0f, (_Float16)1.0f};
+    return __builtin_amdgcn_fdot2(a, one, acc, false);
+  }
+  __device__ static unsigned short bits(float x) { return __builtin_bit_cast(unsigned short, (_Float16)x); }
+};
+
+// 16-byte-chunk swizzle of LDS row r (r & 15 is all that matters).
+//  D = 128 (16 chunks/row, a row spans all 64 banks): a bijection on r & 15 so
+//    the 16 rows of a K read hit 16 distinct chunks, and bits 2-3 = r & 3 so
+//    the 4 rows of a transposing V read land in 4 distinct 64-byte quarters.
+//  D = 64 (8 chunks/row, 2 rows per bank line): a bijection on (r >> 1) & 7
+//    with bit 2 = (r >> 1) & 1 so rows r and r + 2 of a V read differ.
+template <int D>
+__device__ __forceinline__ int swz(int r) {
+  if constexpr (D == 128) {
+    return ((r & 3) << 2) | ((r >> 2) & 3);
+  } else {
+    return (((r >> 1) & 1) << 2) | (((r >> 2) & 1) << 1) | ((r >> 3) & 1);
+  }
+}
+
+__device__ __forceinline__ void dma16(const void* g, lds_char* l) {
+  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)l, 16, 0, 0);
+}
+
+__device__ __forceinline__ void wait_vm0() {
+  // s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima).
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+}
+
+template <int D, typename E>
+__global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
+  using O = Ops<E>;
+  using v8 = typename O::v8;
+  using v2 = typename O::v2;
+  constexpr int RB = D * 2;               // bytes per K/V row
+  constexpr int NCH = RB / 16;            // 16-byte chunks per row
+  constexpr int TILE = kBN * RB;          // bytes of one K or V block
+  constexpr int STAGE = 2 * TILE;
+  constexpr int NI = TILE / 1024;         // 1 KiB DMA instructions per block
+  constexpr int NIW = NI / kWaves;        // per wave
+  constexpr int ND = D / 16;              // MFMA k-steps of S
+  constexpr int NT = D / 32;              // 32-wide d tiles of O
+  static_assert(NI % kWaves == 0, "tile must split evenly over waves");
+
+  __shared__ __attribute__((aligned(1024))) char smem_raw[2 * STAGE];
+  lds_char* smem = (lds_char*)smem_raw;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int h = lane >> 5;        // half of the wave
+  const int i32 = lane & 31;      // query row of this lane within the wave
+
+  // XCD-aware work order: consecutive work items stay on one XCD (shared L2).
+  int w;
+  {
+    const int b = blockIdx.x;
+    const int per = p.total_work / kXcds, rem = p.total_work % kXcds;
+    const int x = b % kXcds, idx = b / kXcds;
+    w = x * per + (x < rem ? x : rem) + idx;
+  }
+  const int tslot = w % p.n_tiles;
+  const int rest = w / p.n_tiles;
+  const int head = rest % p.H;
+  const int batch = rest / p.H;
+  const int tile = tslot < p.n_tt ? p.n_vt + tslot : tslot - p.n_tt;  // text tiles (longest) first
+  const bool text = tile >= p.n_vt;
+  const int hk = head / p.group;
+
+  const char* qbase;
+  char* obase;
+  int64_t qrs, ors;
+  int nrows;
+  int64_t r0;
+  float* lse;
+  if (!text) {
+    qbase = p.q + 2 * (batch * p.q_str[0] + head * p.q_str[2]);
+    obase = p.o + 2 * (batch * p.o_str[0] + head * p.o_str[2]);
+    qrs = 2 * p.q_str[1];
+    ors = 2 * p.o_str[1];
+    nrows = p.n_q;
+    r0 = (int64_t)tile * kBM;
+    lse = p.lse ? p.lse + ((int64_t)batch * p.H + head) * p.n_q : nullptr;
+  } else {
+    qbase = p.qt + 2 * (batch * p.qt_str[0] + head * p.qt_str[2]);
+    obase = p.ot + 2 * (batch * p.ot_str[0] + head * p.ot_str[2]);
+    qrs = 2 * p.qt_str[1];
+    ors = 2 * p.ot_str[1];
+    nrows = p.n_tq;
+    r0 = (int64_t)(tile - p.n_vt) * kBM;
+    lse = p.lse_t ? p.lse_t + ((int64_t)batch * p.H + head) * p.n_tq : nullptr;
+  }
+  const int e0 = p.tile_indptr[tile], e1 = p.tile_indptr[tile + 1];
+
+  const char* kb0 = p.k + 2 * (batch * p.k_str[0] + hk * p.k_str[2]);
+  const char* vb0 = p.v + 2 * (batch * p.v_str[0] + hk * p.v_str[2]);
+  const char* kb1 = p.n_x ? p.kx + 2 * (batch * p.kx_str[0] + hk * p.kx_str[2]) : kb0;
+  const char* vb1 = p.n_x ? p.vx + 2 * (batch * p.vx_str[0] + hk * p.vx_str[2]) : vb0;
+  const int64_t krs0 = 2 * p.k_str[1], vrs0 = 2 * p.v_str[1];
+  const int64_t krs1 = 2 * p.kx_str[1], vrs1 = 2 * p.vx_str[1];
+
+  // Per-lane DMA geometry: instruction ii of this wave covers LDS bytes
+  // [(wave*NIW + ii) KiB, +1 KiB); lane -> (row, logical chunk).
+  int dma_row[NIW], dma_chunk[NIW];
+#pragma unroll
+  for (int ii = 0; ii < NIW; ++ii) {
+    const int pos = (wave * NIW + ii) * 64 + lane;
+    const int r = pos / NCH, pc = pos % NCH;
+    dma_row[ii] = r;
+    dma_chunk[ii] = pc ^ swz<D>(r);
+  }
+
+  auto issue = [&](int e, int stage) {
+    const uint2 ent = p.entries[e];
+    const bool extra = (ent.x >> 31) != 0;
+    const int64_t k0 = (int64_t)(ent.x & 0x7fffffffu) * kBN;
+    const char* kb = extra ? kb1 : kb0;
+    const char* vb = extra ? vb1 : vb0;
+    const int64_t krs = extra ? krs1 : krs0, vrs = extra ? vrs1 : vrs0;
+    const int64_t nsrc = extra ? p.n_x : p.n_k;
+    lds_char* ks = smem + stage * STAGE;
+    lds_char* vs = ks + TILE;
+#pragma unroll
+    for (int ii = 0; ii < NIW; ++ii) {
+      int64_t key = k0 + dma_row[ii];
+      key = key < nsrc ? key : nsrc - 1;
+      const int off = (wave * NIW + ii) * 1024;
+      dma16(kb + key * krs + dma_chunk[ii] * 16, ks + off);
+      dma16(vb + key * vrs + dma_chunk[ii] * 16, vs + off);
+    }
+  };
+
+  // Q fragments (B operand of S^T = K Q^T): row i32 of this wave, d = 16c + 8h .. +7.
+  v8 qf[ND];
+  const int64_t my_row = r0 + 32 * wave + i32;
+  {
+    const int64_t qr = my_row < nrows ? my_row : (int64_t)nrows - 1;
+    const char* qp = qbase + qr * qrs + 16 * h;
+#pragma unroll
+    for (int c = 0; c < ND; ++c) qf[c] = *reinterpret_cast<const v8*>(qp + 32 * c);
+  }
+
+  // LDS read offsets.
+  const int sw_k = swz<D>(i32 & 15);
+  int koff[ND];
+#pragma unroll
+  for (int c = 0; c < ND; ++c) koff[c] = i32 * RB + ((((2 * c + h) ^ sw_k)) << 4);
+  const int g16 = lane & 15;
+  const int rowA = 4 * h + (g16 >> 2);            // + 16*s (+8 for the second read)
+  const int sw_a = swz<D>(rowA), sw_b = swz<D>(rowA + 8);
+  const int dgrp = (lane >> 4) & 1;
+  int voffA[NT], voffB[NT];
+#pragma unroll
+  for (int dt = 0; dt < NT; ++dt) {
+    const int chunk = 4 * dt + 2 * dgrp + ((lane & 3) >> 1);
+    const int inb = (lane & 1) * 8;
+    voffA[dt] = rowA * RB + ((chunk ^ sw_a) << 4) + inb;
+    voffB[dt] = (rowA + 8) * RB + ((chunk ^ sw_b) << 4) + inb;
+  }
+
+  floatx16 oacc[NT];
+#pragma unroll
+  for (int dt = 0; dt < NT; ++dt) oacc[dt] = floatx16{0};
+  float m_run = -1e30f;    // running max of s*scale*log2(e)
+  float l_run = 0.f;       // this lane's share of the row sum
+  const float cs = p.scale_log2;
+  const int my_tile_row = 32 * wave + i32;
+
+  if (e0 < e1) issue(e0, 0);
+  for (int e = e0; e < e1; ++e) {
+    const int stage = (e - e0) & 1;
+    wait_vm0();
+    __syncthreads();
+    if (e + 1 < e1) issue(e + 1, stage ^ 1);
+    const uint2 ent = p.entries[e];
+    const lds_char* ks = smem + stage * STAGE;
+    const lds_char* vs = ks + TILE;
+
+    // S^T for keys [0, 32) and [32, 64) of the block.
+    floatx16 s0 = floatx16{0}, s1 = floatx16{0};
+#pragma unroll
+    for (int c = 0; c < ND; ++c) {
+      const v8 a0 = *reinterpret_cast<const __attribute__((address_space(3))) v8*>(ks + koff[c]);
+      const v8 a1 = *reinterpret_cast<const __attribute__((address_space(3))) v8*>(ks + koff[c] + 32 * RB);
+      s0 = O::mfma(a0, qf[c], s0);
+      s1 = O::mfma(a1, qf[c], s1);
+    }
+
+    // Masks.  Register r of sub-tile t holds key 32t + 8(r/4) + 4h + r%4.
+    const uint32_t desc = ent.y;
+    const uint32_t kind = desc & 3u;
+    if (kind == kKindTwoPart) {
+      const int bits = (desc >> 2) & 0xF;
+      const int kb = (int)((desc >> 8) & 0xFF) - 4 * h;
+      const int qs = (desc >> 16) & 0xFF;
+      const bool rb = my_tile_row >= qs;
+      const bool lo_ok = (bits >> (rb ? 2 : 0)) & 1;
+      const bool hi_ok = (bits >> (rb ? 3 : 1)) & 1;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int kk0 = 8 * (r >> 2) + (r & 3);
+        const bool k0ok = (kk0 < kb) ? lo_ok : hi_ok;
+        const bool k1ok = (kk0 + 32 < kb) ? lo_ok : hi_ok;
+        s0[r] = k0ok ? s0[r] : -INFINITY;
+        s1[r] = k1ok ? s1[r] : -INFINITY;
+      }
+    } else if (kind == kKindGeneric) {
+      const bool extra = (ent.x >> 31) != 0;
+      const int64_t k0 = (int64_t)(ent.x & 0x7fffffffu) * kBN;
+      const int64_t nsrc = extra ? p.n_x : p.n_k;
+      const int64_t qtok = p.q_tok0 + (my_row < nrows ? my_row : (int64_t)nrows - 1);
+      const int qf_row = (int)(qtok / p.R) - p.q_frame0;
+      const uint32_t* relrow = p.rel + (int64_t)qf_row * p.words;
+#pragma unroll
+      for (int r = 0; r < 32; ++r) {
+        const int kk = 32 * (r >> 4) + 8 * ((r & 15) >> 2) + 4 * h + (r & 3);
+        const int64_t key = k0 + kk;
+        bool ok = key < nsrc;
+        if (ok) {
+          const int64_t kf = (p.k_tok0 + key) / p.C;
+          ok = (kf >> 5) < p.words && ((relrow[kf >> 5] >> (kf & 31)) & 1u);
+        }
+        if (r < 16) s0[r] = ok ? s0[r] : -INFINITY;
+        else s1[r - 16] = ok ? s1[r - 16] : -INFINITY;
+      }
+    }
+
+    // Block row max (both halves), lazy rescale.
+    float mx = fmaxf(fmaxf(s0[0], s0[1]), s1[0]);
+#pragma unroll
+    for (int r = 2; r < 16; ++r) mx = fmaxf(fmaxf(mx, s0[r]), s1[r]);
+    mx = fmaxf(mx, s1[1]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float mxs = mx * cs;
+    if (__builtin_amdgcn_ballot_w64(mxs > m_run + 8.0f)) {
+      const float m_new = fmaxf(m_run, mxs);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < NT; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
+      m_run = m_new;
+    }
+
+    // P = 2^(s*cs - m), packed to the MFMA B operand of each 16-key step.
+    v8 pb[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const floatx16& src = (s < 2) ? s0 : s1;
+      const int base = 8 * (s & 1);
+      v2 pk[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float a = __builtin_amdgcn_exp2f(__builtin_fmaf(src[base + 2 * j], cs, -m_run));
+        const float b = __builtin_amdgcn_exp2f(__builtin_fmaf(src[base + 2 * j + 1], cs, -m_run));
+        pk[j] = O::pack(a, b);
+        l_run = O::dot2(pk[j], l_run);
+      }
+      pb[s] = v8{pk[0][0], pk[0][1], pk[1][0], pk[1][1], pk[2][0], pk[2][1], pk[3][0], pk[3][1]};
+    }
+
+    // O^T += V^T P^T.
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+#pragma unroll
+      for (int dt = 0; dt < NT; ++dt) {
+        const shortx4 ta = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) shortx4*)(vs + voffA[dt] + 16 * s * RB));
+        const shortx4 tb = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) shortx4*)(vs + voffB[dt] + 16 * s * RB));
+        const shortx8 t8 = shortx8{ta[0], ta[1], ta[2], ta[3], tb[0], tb[1], tb[2], tb[3]};
+        oacc[dt] = O::mfma(__builtin_bit_cast(v8, t8), pb[s], oacc[dt]);
+      }
+    }
+  }
+
+  // Epilogue: combine the row sum of both halves, normalise, store.
+  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  if (my_row < nrows) {
+    const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+    char* op = obase + my_row * ors;
+#pragma unroll
+    for (int dt = 0; dt < NT; ++dt) {
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq) {
+        const int d0 = 32 * dt + 8 * rq + 4 * h;
+        uint2 pk;
+        pk.x = (uint32_t)O::bits(oacc[dt][4 * rq] * inv) | ((uint32_t)O::bits(oacc[dt][4 * rq + 1] * inv) << 16);
+        pk.y = (uint32_t)O::bits(oacc[dt][4 * rq + 2] * inv) | ((uint32_t)O::bits(oacc[dt][4 * rq + 3] * inv) << 16);
+        *reinterpret_cast<uint2*>(op + 2 * d0) = pk;
+      }
+    }
+    if (lse && h == 0) {
+      lse[my_row] = l_tot > 0.f ? (m_run + __log2f(l_tot)) * 0.69314718055994530942f : -INFINITY;
+    }
+  }
+}
+
+template <int D, typename E>
+int launch(const AttnParams& prm, hipStream_t stream) {
+  hipLaunchKernelGGL((attn_fwd_kernel<D, E>), dim3(prm.total_work), dim3(kThreads), 0, stream, prm);
+  return launch_status("lvsa_attn_fwd");
+}
+
+bool aligned16(const void* ptr, const int64_t* str, int n) {
+  if (((uintptr_t)ptr) % 16) return false;
+  for (int i = 0; i < n; ++i)
+    if ((str[i] * 2) % 16) return false;
+  return true;
+}
+
+}  // namespace
+}  // namespace lvsa
+
+using namespace lvsa;
+
+extern "C" int lvsa_attn_fwd(const lvsa_attn_args* a, hipStream_t stream) {
+  clear_error();
+  LVSA_REQUIRE(a != nullptr, LVSA_ERR_INVALID_ARG, "lvsa_attn_fwd: null args");
+  LVSA_REQUIRE(a->D == 64 || a->D == 128, LVSA_ERR_UNSUPPORTED, "lvsa_attn_fwd: head_dim %d not supported (64, 128)",
+               a->D);
+  LVSA_REQUIRE(a->dtype == LVSA_BF16 || a->dtype == LVSA_FP16, LVSA_ERR_UNSUPPORTED, "lvsa_attn_fwd: dtype %d",
+               a->dtype);
+  LVSA_REQUIRE(a->B >= 1 && a->H >= 1 && a->Hkv >= 1 && a->H % a->Hkv == 0, LVSA_ERR_INVALID_ARG,
+               "lvsa_attn_fwd: B=%d H=%d Hkv=%d (H must be a multiple of Hkv)", a->B, a->H, a->Hkv);
+  LVSA_REQUIRE(a->n_q >= 0 && a->n_k >= 0 && a->n_x >= 0 && a->n_tq >= 0, LVSA_ERR_INVALID_ARG,
+               "lvsa_attn_fwd: negative length");
+  LVSA_REQUIRE(a->tile_indptr && a->entries, LVSA_ERR_INVALID_ARG, "lvsa_attn_fwd: missing plan");
+  const int n_vt = (int)ceil_div(a->n_q, kBM), n_tt = (int)ceil_div(a->n_tq, kBM);
+  LVSA_REQUIRE(a->n_video_tiles == n_vt && a->n_tiles == n_vt + n_tt, LVSA_ERR_INVALID_ARG,
+               "lvsa_attn_fwd: plan has %d/%d tiles, expected %d/%d (block_q must be %d)", a->n_video_tiles,
+               a->n_tiles, n_vt, n_vt + n_tt, kBM);
+  LVSA_REQUIRE(a->n_q == 0 || (a->q && a->o), LVSA_ERR_INVALID_ARG, "lvsa_attn_fwd: null q/o");
+  LVSA_REQUIRE(a->n_tq == 0 || (a->qt && a->ot), LVSA_ERR_INVALID_ARG, "lvsa_attn_fwd: null text q/o");
+  LVSA_REQUIRE(a->n_k == 0 || (a->k && a->v), LVSA_ERR_INVALID_ARG, "lvsa_attn_fwd: null k/v");
+  LVSA_REQUIRE(a->n_x == 0 || (a->kx && a->vx), LVSA_ERR_INVALID_ARG, "lvsa_attn_fwd: null extra k/v");
+  LVSA_REQUIRE(a->n_k + a->n_x > 0 || a->n_tiles == 0, LVSA_ERR_INVALID_ARG, "lvsa_attn_fwd: no keys");
+  bool ok = true;
+  if (a->n_q) ok = ok && aligned16(a->q, a->q_str, 3) && aligned16(a->o, a->o_str, 3);
+  if (a->n_tq) ok = ok && aligned16(a->qt, a->qt_str, 3) && aligned16(a->ot, a->ot_str, 3);
+  if (a->n_k) ok = ok && aligned16(a->k, a->k_str, 3) && aligned16(a->v, a->v_str, 3);
+  if (a->n_x) ok = ok && aligned16(a->kx, a->kx_str, 3) && aligned16(a->vx, a->vx_str, 3);
+  LVSA_REQUIRE(ok, LVSA_ERR_UNSUPPORTED, "lvsa_attn_fwd: tensors must be 16-byte aligned with 16-byte row strides");
+  const int64_t work = (int64_t)a->n_tiles * a->H * a->B;
+  LVSA_REQUIRE(work < (int64_t)INT32_MAX, LVSA_ERR_INVALID_ARG, "lvsa_attn_fwd: too much work");
+  if (work == 0) return LVSA_OK;
+
+  AttnParams p;
+  p.q = (const char*)a->q;
+  p.k = (const char*)a->k;
+  p.v = (const char*)a->v;
+  p.kx = (const char*)a->kx;
+  p.vx = (const char*)a->vx;
+  p.qt = (const char*)a->qt;
+  p.o = (char*)a->o;
+  p.ot = (char*)a->ot;
+  p.lse = a->lse;
+  p.lse_t = a->lse_t;
+  for (int i = 0; i < 3; ++i) {
+    p.q_str[i] = a->q_str[i];
+    p.k_str[i] = a->k_str[i];
+    p.v_str[i] = a->v_str[i];
+    p.kx_str[i] = a->kx_str[i];
+    p.vx_str[i] = a->vx_str[i];
+    p.qt_str[i] = a->qt_str[i];
+    p.o_str[i] = a->o_str[i];
+    p.ot_str[i] = a->ot_str[i];
+  }
+  p.B = a->B;
+  p.H = a->H;
+  p.Hkv = a->Hkv;
+  p.group = a->H / a->Hkv;
+  p.n_q = a->n_q;
+  p.n_k = a->n_k;
+  p.n_x = a->n_x;
+  p.n_tq = a->n_tq;
+  p.scale_log2 = a->scale * 1.4426950408889634f;
+  p.tile_indptr = a->tile_indptr;
+  p.entries = reinterpret_cast<const uint2*>(a->entries);
+  p.n_tiles = a->n_tiles;
+  p.n_vt = n_vt;
+  p.n_tt = n_tt;
+  p.rel = a->rel;
+  p.words = a->words;
+  p.R = a->R > 0 ? a->R : 1;
+  p.C = a->C > 0 ? a->C : 1;
+  p.q_frame0 = a->q_frame0;
+  p.q_tok0 = a->q_tok0;
+  p.k_tok0 = a->k_tok0;
+  p.total_work = (int)work;
+  if (a->D == 128) return a->dtype == LVSA_BF16 ? launch<128, __bf16>(p, stream) : launch<128, _Float16>(p, stream);
+  return a->dtype == LVSA_BF16 ? launch<64, __bf16>(p, stream) : launch<64, _Float16>(p, stream);
+}

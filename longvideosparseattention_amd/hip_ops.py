@@ -1,0 +1,286 @@
+"""Torch-facing wrappers of the C-ABI entry points (device memory + streams).
+
+Torch is used only for device allocation and the current stream; every
+computation is one of the HIP kernels of ``liblvsa_amd.so``.  Inputs must be
+device tensors: there is no CPU path.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import math
+from dataclasses import dataclass
+from typing import Optional, Sequence, Tuple
+
+import torch
+
+from . import _capi as capi
+
+_DTYPES = {torch.bfloat16: capi.LVSA_BF16, torch.float16: capi.LVSA_FP16}
+SUPPORTED_HEAD_DIMS = (64, 128)
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _require_device(t: torch.Tensor, name: str) -> None:
+    if not isinstance(t, torch.Tensor) or t.device.type != "cuda":
+        raise RuntimeError(
+            f"{name} must be a GPU (HIP) tensor: the LVSA MI355X backend has no CPU path "
+            f"(got {getattr(t, 'device', type(t))})"
+        )
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+# ───────────────────────────── mask builder ────────────────────────────────
+
+
+@dataclass
+class DeviceMask:
+    """Device outputs of ``lvsa_mask_build`` (see include/lvsa_amd.h)."""
+
+    frame_indptr: torch.Tensor      # [n_rows+1] int32
+    frame_indices: torch.Tensor     # [max_nnz] int32 (first nnz valid)
+    compact_frames: torch.Tensor    # [T] int32
+    global_frames: torch.Tensor     # [T] int32
+    window_bounds: torch.Tensor     # [T, 2] int32
+    rel_full: torch.Tensor          # [n_local, words] int32 (uint32 bit patterns)
+    rel_window: torch.Tensor        # [n_local, words]
+    info: torch.Tensor              # [8] int32
+    n_rows: int
+    n_local: int
+    words: int
+    local_seq: int
+    global_token_start: int
+
+
+def mask_params(T: int, P: int, W: int, n_first: int, kfi: Optional[int], offset: int = 0,
+                expand: bool = True, rank: int = 0, world: int = 1,
+                guards: Sequence[int] = ()) -> capi.MaskParams:
+    if not 1 <= T <= capi.LVSA_MAX_FRAMES:
+        raise ValueError(f"total_latent_frames={T} outside [1, {capi.LVSA_MAX_FRAMES}]")
+    p = capi.MaskParams()
+    p.T, p.P, p.window, p.n_first = T, P, W, n_first
+    p.kfi = int(kfi) if (kfi is not None and kfi > 0) else 0
+    p.offset, p.expand, p.rank, p.world = int(offset), int(bool(expand)), rank, world
+    for g in guards:
+        if 0 <= g < T:
+            p.guard_bits[g >> 5] |= 1 << (g & 31)
+    return p
+
+
+def mask_sizes(p: capi.MaskParams) -> capi.MaskSizes:
+    s = capi.MaskSizes()
+    capi.check("lvsa_mask_sizes_query", capi.lib().lvsa_mask_sizes_query(C.byref(p), C.byref(s)))
+    return s
+
+
+def mask_build(p: capi.MaskParams, device: torch.device) -> DeviceMask:
+    device = torch.device(device)
+    if device.type != "cuda":
+        raise RuntimeError("lvsa_mask_build runs on the GPU only")
+    s = mask_sizes(p)
+    i32 = dict(dtype=torch.int32, device=device)
+    T = p.T
+    dm = DeviceMask(
+        frame_indptr=torch.empty(s.n_rows + 1, **i32),
+        frame_indices=torch.empty(max(s.max_nnz, 1), **i32),
+        compact_frames=torch.empty(T, **i32),
+        global_frames=torch.empty(T, **i32),
+        window_bounds=torch.empty(T, 2, **i32),
+        rel_full=torch.empty(s.n_local, s.words, **i32),
+        rel_window=torch.empty(s.n_local, s.words, **i32),
+        info=torch.empty(8, **i32),
+        n_rows=s.n_rows, n_local=s.n_local, words=s.words,
+        local_seq=s.local_seq, global_token_start=s.global_token_start,
+    )
+    out = capi.MaskOut(
+        dm.frame_indptr.data_ptr(), dm.frame_indices.data_ptr(), dm.compact_frames.data_ptr(),
+        dm.global_frames.data_ptr(), dm.window_bounds.data_ptr(), dm.rel_full.data_ptr(),
+        dm.rel_window.data_ptr(), dm.info.data_ptr(),
+    )
+    with torch.cuda.device(device):
+        capi.check("lvsa_mask_build", capi.lib().lvsa_mask_build(C.byref(p), C.byref(out), _stream(device)))
+    return dm
+
+
+# ────────────────────────────── block plan ─────────────────────────────────
+
+
+@dataclass
+class BlockPlan:
+    """Block-sparse CSR over query tiles (``lvsa_plan_build``)."""
+
+    tile_indptr: torch.Tensor   # [n_tiles+1] int32
+    entries: torch.Tensor       # [max_entries, 2] int32 (uint32 bit patterns)
+    status: torch.Tensor        # [4] int32: overflow flag, true entry count
+    n_tiles: int
+    n_video_tiles: int
+    params: capi.PlanParams
+    rel: Optional[torch.Tensor]  # keeps the relation bitmap alive
+
+    @property
+    def block_q(self) -> int:
+        return self.params.block_q
+
+    @property
+    def block_k(self) -> int:
+        return self.params.block_k
+
+
+def plan_build(rel: Optional[torch.Tensor], *, n_q: int, n_k: int, n_x: int = 0, n_tq: int = 0,
+               R: int = 1, Cf: int = 1, q_tok0: int = 0, k_tok0: int = 0, q_frame0: int = 0,
+               max_row_frames: int = 0, block_q: int = capi.ATTN_BLOCK_Q, block_k: int = capi.ATTN_BLOCK_K,
+               device: Optional[torch.device] = None) -> BlockPlan:
+    """Refine a frame relation (bitmap rows x words, int32) to token blocks."""
+    if rel is not None:
+        _require_device(rel, "relation bitmap")
+        device = rel.device
+        rel = rel.contiguous()
+    if device is None or torch.device(device).type != "cuda":
+        raise RuntimeError("lvsa_plan_build runs on the GPU only")
+    device = torch.device(device)
+    p = capi.PlanParams()
+    p.n_q, p.n_k, p.n_x, p.n_tq = n_q, n_k, n_x, n_tq
+    p.R, p.C = R, Cf
+    p.q_tok0, p.k_tok0, p.q_frame0 = q_tok0, k_tok0, q_frame0
+    p.rel_rows = rel.shape[0] if rel is not None else 0
+    p.words = rel.shape[1] if rel is not None else 0
+    p.rel = rel.data_ptr() if rel is not None else None
+    p.block_q, p.block_k = block_q, block_k
+    sz = capi.PlanSizes()
+    capi.check("lvsa_plan_sizes_query", capi.lib().lvsa_plan_sizes_query(C.byref(p), max_row_frames, C.byref(sz)))
+    i32 = dict(dtype=torch.int32, device=device)
+    indptr = torch.empty(sz.n_tiles + 1, **i32)
+    entries = torch.empty(max(sz.max_entries, 1), 2, **i32)
+    status = torch.empty(max(sz.workspace_bytes // 4, 4), **i32)
+    with torch.cuda.device(device):
+        capi.check("lvsa_plan_build", capi.lib().lvsa_plan_build(
+            C.byref(p), indptr.data_ptr(), entries.data_ptr(), sz.max_entries,
+            status.data_ptr(), status.numel() * 4, _stream(device)))
+    return BlockPlan(indptr, entries, status, sz.n_tiles, sz.n_video_tiles, p, rel)
+
+
+# ─────────────────────────── attention forward ─────────────────────────────
+
+
+def _prep(t: torch.Tensor, name: str, dtype: torch.dtype) -> torch.Tensor:
+    _require_device(t, name)
+    if t.dim() != 4:
+        raise ValueError(f"{name} must be [B, S, H, D], got shape {tuple(t.shape)}")
+    if t.dtype != dtype:
+        raise TypeError(f"{name} has dtype {t.dtype}, expected {dtype}")
+    ok = t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and all((s * t.element_size()) % 16 == 0
+                                                              for s in t.stride()[:3])
+    return t if ok else t.contiguous()
+
+
+def _str3(t: Optional[torch.Tensor]):
+    return capi._Str3(*(t.stride()[:3] if t is not None else (0, 0, 0)))
+
+
+def attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, plan: BlockPlan, *,
+             kx: Optional[torch.Tensor] = None, vx: Optional[torch.Tensor] = None,
+             qt: Optional[torch.Tensor] = None, scale: Optional[float] = None,
+             return_lse: bool = False, out: Optional[torch.Tensor] = None,
+             out_t: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, Optional[torch.Tensor],
+                                                           Optional[torch.Tensor], Optional[torch.Tensor]]:
+    """Block-sparse attention over ``plan``: returns ``(o, o_text, lse, lse_text)``.
+
+    ``lse`` is the natural-log log-sum-exp ``[B, H, S]`` (fp32) when requested.
+    """
+    dtype = q.dtype
+    if dtype not in _DTYPES:
+        raise TypeError(f"unsupported dtype {dtype}: bf16 or fp16 inputs (fp32 callers cast first)")
+    q = _prep(q, "query", dtype)
+    k = _prep(k, "key", dtype)
+    v = _prep(v, "value", dtype)
+    B, n_q, H, D = q.shape
+    Hkv = k.shape[2]
+    if D not in SUPPORTED_HEAD_DIMS:
+        raise ValueError(f"head_dim {D} not supported by the gfx950 kernel (supported: {SUPPORTED_HEAD_DIMS})")
+    if k.shape[0] != B or k.shape[3] != D or v.shape != k.shape:
+        raise ValueError(f"key/value shapes {tuple(k.shape)} / {tuple(v.shape)} do not match query {tuple(q.shape)}")
+    if H % Hkv:
+        raise ValueError(f"num heads {H} must be a multiple of kv heads {Hkv}")
+    n_x = 0
+    if kx is not None and kx.shape[1] > 0:
+        kx = _prep(kx, "extra key", dtype)
+        vx = _prep(vx, "extra value", dtype)
+        if kx.shape[0] != B or kx.shape[2] != Hkv or kx.shape[3] != D or vx.shape != kx.shape:
+            raise ValueError("extra key/value shape mismatch")
+        n_x = kx.shape[1]
+    else:
+        kx = vx = None
+    n_tq = 0
+    if qt is not None and qt.shape[1] > 0:
+        qt = _prep(qt, "text query", dtype)
+        if qt.shape[0] != B or qt.shape[2] != H or qt.shape[3] != D:
+            raise ValueError("text query shape mismatch")
+        n_tq = qt.shape[1]
+    else:
+        qt = None
+    pp = plan.params
+    if (pp.n_q, pp.n_k, pp.n_x, pp.n_tq) != (n_q, k.shape[1], n_x, n_tq):
+        raise ValueError(
+            f"plan built for (n_q, n_k, n_x, n_tq)={(pp.n_q, pp.n_k, pp.n_x, pp.n_tq)}, "
+            f"called with {(n_q, k.shape[1], n_x, n_tq)}")
+    if out is None:
+        out = torch.empty_like(q, memory_format=torch.contiguous_format)
+    if qt is not None and out_t is None:
+        out_t = torch.empty_like(qt, memory_format=torch.contiguous_format)
+    lse = torch.empty(B, H, n_q, dtype=torch.float32, device=q.device) if return_lse else None
+    lse_t = (torch.empty(B, H, n_tq, dtype=torch.float32, device=q.device)
+             if (return_lse and qt is not None) else None)
+    a = capi.AttnArgs()
+    a.q, a.k, a.v = q.data_ptr(), k.data_ptr(), v.data_ptr()
+    a.kx, a.vx, a.qt = _ptr(kx), _ptr(vx), _ptr(qt)
+    a.o, a.ot = out.data_ptr(), _ptr(out_t)
+    a.lse, a.lse_t = _ptr(lse), _ptr(lse_t)
+    a.q_str, a.k_str, a.v_str = _str3(q), _str3(k), _str3(v)
+    a.kx_str, a.vx_str, a.qt_str = _str3(kx), _str3(vx), _str3(qt)
+    a.o_str, a.ot_str = _str3(out), _str3(out_t)
+    a.B, a.H, a.Hkv, a.D = B, H, Hkv, D
+    a.n_q, a.n_k, a.n_x, a.n_tq = n_q, k.shape[1], n_x, n_tq
+    a.scale = float(scale) if scale is not None else 1.0 / math.sqrt(D)
+    a.dtype = _DTYPES[dtype]
+    a.tile_indptr, a.entries = plan.tile_indptr.data_ptr(), plan.entries.data_ptr()
+    a.n_tiles, a.n_video_tiles = plan.n_tiles, plan.n_video_tiles
+    a.rel = pp.rel
+    a.words, a.R, a.C, a.q_frame0 = pp.words, pp.R, pp.C, pp.q_frame0
+    a.q_tok0, a.k_tok0 = pp.q_tok0, pp.k_tok0
+    with torch.cuda.device(q.device):
+        capi.check("lvsa_attn_fwd", capi.lib().lvsa_attn_fwd(C.byref(a), _stream(q.device)))
+    return out, out_t, lse, lse_t
+
+
+# ───────────────────────────── frame gather ────────────────────────────────
+
+
+def gather_frames(src: torch.Tensor, frames: torch.Tensor, P: int) -> torch.Tensor:
+    """``dst[b, i*P + t] = src[b, frames[i]*P + t]`` on the GPU."""
+    _require_device(src, "source")
+    if src.dim() != 4:
+        raise ValueError("source must be [B, S, H, D]")
+    if src.stride(-1) != 1:
+        src = src.contiguous()
+    frames = frames.to(device=src.device, dtype=torch.int32)
+    B, _, H, D = src.shape
+    n = frames.numel()
+    dst = src.new_empty(B, n * P, H, D)
+    if n == 0:
+        return dst
+    es = src.element_size()
+    if es not in (2, 4):
+        raise TypeError(f"unsupported element size {es}")
+    sstr = (C.c_int64 * 3)(*src.stride()[:3])
+    dstr = (C.c_int64 * 3)(*dst.stride()[:3])
+    with torch.cuda.device(src.device):
+        capi.check("lvsa_gather_frames", capi.lib().lvsa_gather_frames(
+            src.data_ptr(), sstr, dst.data_ptr(), dstr, frames.data_ptr(), n, P, B, H, D, es,
+            _stream(src.device)))
+    return dst
