@@ -1,0 +1,206 @@
+"""Benchmark of the LVSA block-sparse attention hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config wan4x|wan6x|cog|hv|cpu]
+
+One step = one attention call over one synthetic batch at the configuration's
+full single-GPU shape, with the keyframe grid rotated by the step index
+(offset = step % kfi), as in a denoising loop.  The per-offset masks and
+block plans are built on the GPU before the timed region (they are built once
+per denoising step and shared by every layer in a real pipeline); their cost
+is reported separately.  Inputs are resident in HBM when timing starts.
+
+Prints ONE JSON line: metric/value (effective TFLOP/s on active 128-blocks,
+BASELINE's metric), ms per call, the roofline of the attention kernel
+(algorithmic FLOPs per launch / HIP-event launch time vs the 2.5 PFLOP/s
+dense bf16 MFMA peak of MI355X) and a CPU baseline (the repository's fp32
+CPU restatement timed on the host cores over a bounded sample).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+import longvideosparseattention_amd as lv  # noqa: E402
+from longvideosparseattention_amd import flops as lvflops  # noqa: E402
+
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+HBM_PEAK_GBS = 8000.0
+
+CONFIGS = {
+    # name: T, P, H, D, W, kfi, offsets, n_text, block, workload
+    "wan4x": (84, 1560, 12, 128, 2, 8, list(range(8)), 0, 128,
+              "Wan2.1-1.3B 4x horizon self-attention (84 latent frames x 1560 tokens)"),
+    "wan6x": (121, 1560, 12, 128, 2, 8, list(range(8)), 0, 128,
+              "Wan2.1-1.3B 6x horizon self-attention (121 latent frames x 1560 tokens)"),
+    "cog": (13, 1350, 48, 64, 1, 4, [0], 226, 64,
+            "CogVideoX-5B joint attention (226 text + 13 x 1350 video tokens)"),
+    "hv": (49, 1590, 16, 128, 2, 8, list(range(8)), 256, 128,
+           "HunyuanVideo-1.5 480p 1.5x dual-stream attention (49 x 1590 video + 256 text)"),
+    "cpu": (9, 256, 12, 128, 1, 4, [3], 0, 64,
+            "reference CPU configuration (9 latent frames x 256 tokens)"),
+}
+
+
+def parse(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=24)
+    ap.add_argument("--warmup", type=int, default=4)
+    ap.add_argument("--config", default="wan4x", choices=sorted(CONFIGS))
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-baseline sample budget")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--seed", type=int, default=0)
+    return ap.parse_args(argv)
+
+
+def cpu_baseline(q, k, v, qt, kt, vt, meta, budget_s: float):
+    """Time the fp32 CPU restatement (per-frame gather + dense attention) of the
+    same call on the host cores over a bounded sample of (head, query frame)
+    pairs; return its throughput in effective TFLOP/s (token-exact work)."""
+    from oracle import attention as oa  # CPU-baseline leg only
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    P = meta.num_patches
+    T = meta.total_latent_frames
+    rows = [set(meta._attended_rows[f]) for f in range(T)]
+    D = q.shape[3]
+    work = 0
+    n_pairs = 0
+    t0 = time.perf_counter()
+    h = 0
+    while time.perf_counter() - t0 < budget_s and h < q.shape[2]:
+        for f in range(T):
+            qs = slice(f * P, (f + 1) * P)
+            parts_k = [k[:, g * P:(g + 1) * P, h:h + 1] for g in sorted(rows[f])]
+            parts_v = [v[:, g * P:(g + 1) * P, h:h + 1] for g in sorted(rows[f])]
+            if kt is not None:
+                parts_k.append(kt[:, :, h:h + 1])
+                parts_v.append(vt[:, :, h:h + 1])
+            kc, vc = torch.cat(parts_k, 1), torch.cat(parts_v, 1)
+            oa.dense_attention(q[:, qs, h:h + 1], kc, vc)
+            work += 4 * D * P * kc.shape[1]
+            n_pairs += 1
+            if time.perf_counter() - t0 >= budget_s:
+                break
+        h += 1
+    dt = time.perf_counter() - t0
+    return {"value": work / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"{n_pairs} (head, query-frame) pairs of the same call in fp32 "
+                      f"({work / 1e9:.1f} GFLOP token-exact, {dt:.1f} s), text rows excluded"}
+
+
+def main(argv=None) -> int:
+    args = parse(argv)
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build runs the LVSA hot path on ONE GPU; multi-GPU runs are not part of it "
+              "(see DESIGN.md for how the path would shard).", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda", 0)
+    T, P, H, D, W, kfi, offsets, n_text, block, workload = CONFIGS[args.config]
+    N = T * P
+    dt = torch.bfloat16
+
+    # Synthetic inputs: one CPU generator, fp32 randn in order q, k, v, text q, k, v.
+    g = torch.Generator().manual_seed(args.seed)
+    q32, k32, v32 = (torch.randn(1, N, H, D, generator=g) for _ in range(3))
+    qt32 = kt32 = vt32 = None
+    if n_text:
+        qt32, kt32, vt32 = (torch.randn(1, n_text, H, D, generator=g) for _ in range(3))
+    q, k, v = (x.to(dt).to(dev) for x in (q32, k32, v32))
+    qt = kt = vt = None
+    if n_text:
+        qt, kt, vt = (x.to(dt).to(dev) for x in (qt32, kt32, vt32))
+
+    # Per-offset metadata + plans (device), built and timed outside the step loop.
+    metas = {}
+    build_ms = []
+    for off in offsets:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        m = lv.LVSAMetadata.build(total_latent_frames=T, num_patches=P, window_size=W, n_first_frames=1,
+                                  key_frame_interval=kfi, rank=0, world=1, keyframe_offset=off)
+        m.full_plan(dev, N, N, n_text, n_text)
+        torch.cuda.synchronize()
+        build_ms.append(1e3 * (time.perf_counter() - t0))
+        metas[off] = m
+    flops = {off: lvflops.attention_flops(metas[off], dev, block, H, D, n_text) for off in offsets}
+
+    def step(i):
+        m = metas[offsets[i % len(offsets)]]
+        if n_text:
+            return lv.lvsa_attention(q, k, v, m, k_text=kt, v_text=vt, q_text=qt)
+        return lv.lvsa_attention(q, k, v, m)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record()
+    for i in range(args.steps):
+        step(i)
+    ev1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ev_ms = ev0.elapsed_time(ev1) / args.steps
+    ms = 1e3 * wall / args.steps
+    fb = sum(flops[offsets[i % len(offsets)]][0] for i in range(args.steps))
+    fx = sum(flops[offsets[i % len(offsets)]][1] for i in range(args.steps))
+    value = fb / wall / 1e12
+    achieved = fb / (ev_ms * 1e-3 * args.steps) / 1e12
+    bytes_per_call = 4 * (N + n_text) * H * D * 2
+
+    line = {
+        "metric": "block-sparse attn ms/call + effective TFLOP/s (% bf16 MFMA peak), "
+                  + {"wan4x": "Wan 4x shape"}.get(args.config, args.config + " shape"),
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: seeded N(0,1) q/k/v, bf16, RoPE-free; keyframe offset = step % kfi",
+        "config": {"workload": workload, "T": T, "P": P, "heads": H, "head_dim": D, "window": W,
+                   "kfi": kfi, "n_first": 1, "offsets": offsets, "text_tokens": n_text, "block": block,
+                   "batch": 1, "parallelism": "single GPU"},
+        "pct_bf16_mfma_peak": round(100 * value / MFMA_BF16_PEAK_TFLOPS, 2),
+        "tflops_token_exact": round(fx / wall / 1e12, 2),
+        "gflop_per_call_block": round(fb / args.steps / 1e9, 1),
+        "hbm_gbs_algorithmic": round(bytes_per_call / (ms * 1e-3) / 1e9, 1),
+        "mask_and_plan_build_ms": round(sum(build_ms) / len(build_ms), 3),
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
+                     "kernel": "attn_fwd_kernel", "kernel_ms": round(ev_ms, 4)},
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(q.float().cpu(), k.float().cpu(), v.float().cpu(),
+                                            None if qt is None else qt.float().cpu(),
+                                            None if kt is None else kt.float().cpu(),
+                                            None if vt is None else vt.float().cpu(),
+                                            metas[offsets[0]], args.cpu_seconds)
+    else:
+        line["cpu_baseline"] = None
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

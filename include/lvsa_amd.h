@@ -152,6 +152,15 @@ LVSA_API int lvsa_plan_build(const lvsa_plan_params* p, int32_t* tile_indptr, ui
                     int64_t max_entries, void* workspace, int64_t workspace_bytes,
                     hipStream_t stream);
 
+/* Block CSR (row pointers, column ids) -> relation bitmap [n_rows*words]
+ * (bit c of row r set iff column c is listed in row r).  Used to plan a
+ * block-sparse wrapper from the CSR it was given, as FlashInfer's
+ * BlockSparseAttentionWrapper.plan does (lvsa/lvsa_processor.py:805-827;
+ * flashinfer_runner.py:79-94).  status[0] = 1 flags out-of-range columns.
+ * status needs 4 int32 (the last two are scratch).                          */
+LVSA_API int lvsa_csr_to_bitmap(const int32_t* indptr, const int32_t* indices, int32_t n_rows, int32_t n_cols,
+                                uint32_t* bitmap, int32_t words, int32_t* status, hipStream_t stream);
+
 /* ─────────────────────────── attention forward ─────────────────────────── */
 
 typedef struct lvsa_attn_args {

@@ -105,6 +105,8 @@ SIGNATURES = {
     "lvsa_plan_sizes_query": (C.c_int, [C.POINTER(PlanParams), C.c_int32, C.POINTER(PlanSizes)]),
     "lvsa_plan_build": (C.c_int, [C.POINTER(PlanParams), C.c_void_p, C.c_void_p, C.c_int64,
                                   C.c_void_p, C.c_int64, C.c_void_p]),
+    "lvsa_csr_to_bitmap": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int32, C.c_int32, C.c_void_p, C.c_int32,
+                                     C.c_void_p, C.c_void_p]),
     "lvsa_attn_fwd": (C.c_int, [C.POINTER(AttnArgs), C.c_void_p]),
     "lvsa_gather_frames": (C.c_int, [C.c_void_p, C.POINTER(C.c_int64), C.c_void_p, C.POINTER(C.c_int64),
                                      C.c_void_p, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32,

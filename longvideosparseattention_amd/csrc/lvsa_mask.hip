@@ -394,6 +394,25 @@ __global__ void plan_empty_kernel(int32_t* indptr, int32_t* status) {
   status[1] = 0;
 }
 
+// Rows of a block CSR -> relation bitmap (one thread per row).
+__global__ __launch_bounds__(128) void csr_to_bitmap_kernel(const int32_t* indptr, const int32_t* indices,
+                                                            int n_rows, int n_cols, int words, uint32_t* out,
+                                                            int32_t* status) {
+  const int r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= n_rows) return;
+  uint32_t* row = out + (int64_t)r * words;
+  for (int w = 0; w < words; ++w) row[w] = 0u;
+  const int a = indptr[r], b = indptr[r + 1];
+  for (int e = a; e < b; ++e) {
+    const int c = indices[e];
+    if (c >= 0 && c < n_cols) {
+      row[c >> 5] |= 1u << (c & 31);
+    } else {
+      status[0] = 1;  // column out of range: reported, not written
+    }
+  }
+}
+
 // ───────────────────────────── frame gather ────────────────────────────────
 
 template <typename V>
@@ -540,6 +559,21 @@ int lvsa_plan_build(const lvsa_plan_params* p, int32_t* tile_indptr, uint32_t* e
   hipLaunchKernelGGL(plan_tiles_kernel<true>, grid, dim3(kPlanThreads), 0, stream, c, tile_indptr, entries,
                      max_entries);
   return launch_status("lvsa_plan_build");
+}
+
+int lvsa_csr_to_bitmap(const int32_t* indptr, const int32_t* indices, int32_t n_rows, int32_t n_cols,
+                       uint32_t* bitmap, int32_t words, int32_t* status, hipStream_t stream) {
+  clear_error();
+  LVSA_REQUIRE(indptr && bitmap && status, LVSA_ERR_INVALID_ARG, "lvsa_csr_to_bitmap: null pointer");
+  LVSA_REQUIRE(n_rows >= 0 && n_cols >= 0, LVSA_ERR_INVALID_ARG, "lvsa_csr_to_bitmap: negative size");
+  LVSA_REQUIRE(words >= (n_cols + 31) / 32, LVSA_ERR_CAPACITY, "lvsa_csr_to_bitmap: %d words < %d columns", words,
+               n_cols);
+  hipLaunchKernelGGL(plan_empty_kernel, dim3(1), dim3(1), 0, stream, (int32_t*)status + 2, status);
+  if (n_rows == 0) return launch_status("lvsa_csr_to_bitmap");
+  LVSA_REQUIRE(indices != nullptr, LVSA_ERR_INVALID_ARG, "lvsa_csr_to_bitmap: null indices");
+  hipLaunchKernelGGL(csr_to_bitmap_kernel, dim3((unsigned)ceil_div(n_rows, 128)), dim3(128), 0, stream, indptr,
+                     indices, n_rows, n_cols, words, bitmap, status);
+  return launch_status("lvsa_csr_to_bitmap");
 }
 
 int lvsa_gather_frames(const void* src, const int64_t src_str[3], void* dst, const int64_t dst_str[3],

@@ -176,7 +176,8 @@ def _prep(t: torch.Tensor, name: str, dtype: torch.dtype) -> torch.Tensor:
         raise TypeError(f"{name} has dtype {t.dtype}, expected {dtype}")
     ok = t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and all((s * t.element_size()) % 16 == 0
                                                               for s in t.stride()[:3])
-    return t if ok else t.contiguous()
+    # The kernel reads 16-byte row chunks; other layouts are repacked on the device.
+    return t if ok else t.clone(memory_format=torch.contiguous_format)
 
 
 def _str3(t: Optional[torch.Tensor]):
@@ -284,3 +285,23 @@ def gather_frames(src: torch.Tensor, frames: torch.Tensor, P: int) -> torch.Tens
             src.data_ptr(), sstr, dst.data_ptr(), dstr, frames.data_ptr(), n, P, B, H, D, es,
             _stream(src.device)))
     return dst
+
+
+def csr_to_bitmap(indptr: torch.Tensor, indices: torch.Tensor, n_cols: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Block CSR -> relation bitmap ``[n_rows, ceil(n_cols/32)]`` (int32 words) on the GPU.
+
+    Returns ``(bitmap, status)``; ``status[0] == 1`` flags out-of-range columns.
+    """
+    _require_device(indptr, "indptr")
+    device = indptr.device
+    indptr = indptr.to(dtype=torch.int32).contiguous()
+    indices = indices.to(device=device, dtype=torch.int32).contiguous()
+    n_rows = indptr.numel() - 1
+    words = max(1, -(-n_cols // 32))
+    bitmap = torch.empty(max(n_rows, 1), words, dtype=torch.int32, device=device)
+    status = torch.empty(4, dtype=torch.int32, device=device)
+    with torch.cuda.device(device):
+        capi.check("lvsa_csr_to_bitmap", capi.lib().lvsa_csr_to_bitmap(
+            indptr.data_ptr(), indices.data_ptr() if indices.numel() else None, n_rows, n_cols,
+            bitmap.data_ptr(), words, status.data_ptr(), _stream(device)))
+    return bitmap[:n_rows], status

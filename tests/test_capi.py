@@ -1,0 +1,98 @@
+"""The C-ABI library (CPU only: no kernel is launched).
+
+* liblvsa_amd.so loads and exports every function include/lvsa_amd.h declares;
+* the ctypes structures have the C layout (checked against gcc's offsetof);
+* the host-only sizing entry points validate their input and report errors.
+"""
+
+import ctypes as C
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from longvideosparseattention_amd import _capi
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "lvsa_amd.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"LVSA_API\s+[\w\s\*]*?\b(lvsa_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _capi.lib()
+    names = _declared()
+    assert len(names) >= 9
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(names) == set(_capi.SIGNATURES)
+    assert _capi.version() == re.search(r'LVSA_AMD_VERSION "([^"]+)"', HEADER.read_text()).group(1)
+
+
+def test_struct_layout_matches_c(tmp_path):
+    structs = {"lvsa_mask_params": _capi.MaskParams, "lvsa_mask_sizes": _capi.MaskSizes,
+               "lvsa_mask_out": _capi.MaskOut, "lvsa_plan_params": _capi.PlanParams,
+               "lvsa_plan_sizes": _capi.PlanSizes, "lvsa_attn_args": _capi.AttnArgs}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "lvsa_amd.h"', "int main(void) {"]
+    for cname, py in structs.items():
+        lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
+        for fname, _ in py._fields_:
+            lines.append(f'printf("{cname} {fname} %zu\\n", offsetof({cname}, {fname}));')
+    lines.append("return 0; }")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    cc = subprocess.run(["gcc", "-D__HIP_PLATFORM_AMD__", f"-I{ROOT / 'include'}", "-I/opt/rocm/include",
+                         str(src), "-o", str(exe)], capture_output=True, text=True)
+    if cc.returncode != 0:
+        pytest.fail(f"gcc failed: {cc.stderr}")
+    out = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split("\n")
+    got = {}
+    for line in filter(None, out):
+        s, f, v = line.split()
+        got[(s, f)] = int(v)
+    for cname, py in structs.items():
+        assert got[(cname, "size")] == C.sizeof(py), cname
+        for fname, _ in py._fields_:
+            assert got[(cname, fname)] == getattr(py, fname).offset, (cname, fname)
+
+
+def test_mask_sizes_and_errors():
+    lib = _capi.lib()
+    p = _capi.MaskParams(T=84, P=1560, window=2, n_first=1, kfi=8, offset=0, expand=1, rank=0, world=1)
+    s = _capi.MaskSizes()
+    assert lib.lvsa_mask_sizes_query(C.byref(p), C.byref(s)) == 0
+    assert (s.n_rows, s.n_local, s.words, s.local_seq) == (84, 84, 3, 84 * 1560)
+    p.T = 0
+    assert lib.lvsa_mask_sizes_query(C.byref(p), C.byref(s)) == -1
+    assert b"T=0" in lib.lvsa_last_error()
+    p.T, p.world = 5, 2
+    p.P = 3
+    assert lib.lvsa_mask_sizes_query(C.byref(p), C.byref(s)) == -1
+    assert b"divisible by world" in lib.lvsa_last_error()
+
+
+def test_plan_sizes():
+    lib = _capi.lib()
+    p = _capi.PlanParams(n_q=131040, n_k=131040, n_x=0, n_tq=0, R=1560, C=1560, q_tok0=0, k_tok0=0,
+                         q_frame0=0, rel_rows=84, words=3, rel=1, block_q=128, block_k=64)
+    s = _capi.PlanSizes()
+    assert lib.lvsa_plan_sizes_query(C.byref(p), 17, C.byref(s)) == 0
+    assert s.n_tiles == s.n_video_tiles == 1024
+    assert 0 < s.max_entries <= 1024 * 2048
+    p.block_q = 300
+    assert lib.lvsa_plan_sizes_query(C.byref(p), 17, C.byref(s)) == -1
+
+
+def test_attn_rejects_bad_args_without_launching():
+    lib = _capi.lib()
+    a = _capi.AttnArgs()
+    a.D, a.dtype, a.B, a.H, a.Hkv = 96, 0, 1, 2, 2
+    assert lib.lvsa_attn_fwd(C.byref(a), None) == -2
+    assert b"head_dim 96" in lib.lvsa_last_error()
+    a.D, a.H, a.Hkv = 128, 3, 2
+    assert lib.lvsa_attn_fwd(C.byref(a), None) == -1

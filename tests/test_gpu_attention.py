@@ -1,0 +1,265 @@
+"""GPU parity of the block-sparse attention kernel through every entry point.
+
+Reference: the fp32 oracle (``oracle/attention.py``) on the same bf16-rounded
+inputs.  Tolerance (bf16 output vs fp32 reference):
+max |err| <= 2e-2 and mean |err| <= 2e-3.  Inputs follow the BASELINE recipe:
+one CPU generator, seed 0, fp32 randn drawn in order q, k, v, then text q,
+k, v, shapes [B, N, H, D], rounded to the compute dtype.
+"""
+
+import math
+
+import pytest
+import torch
+
+import longvideosparseattention_amd as lv
+from longvideosparseattention_amd import hip_ops
+from oracle import attention as oa
+from oracle import lvsa_mask as om
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS = 2e-2
+MEAN_ABS = 2e-3
+
+
+def _draw(shapes, seed=0, dtype=torch.bfloat16):
+    g = torch.Generator().manual_seed(seed)
+    return [torch.randn(*s, generator=g, dtype=torch.float32).to(dtype) for s in shapes]
+
+
+def _close(got, ref, what, max_abs=MAX_ABS, mean_abs=MEAN_ABS):
+    ref = ref.to(got.device)
+    sel = torch.isfinite(ref)
+    err = (got.float()[sel] - ref[sel]).abs()
+    assert err.numel() > 0
+    mx, mn = err.max().item(), err.mean().item()
+    assert mx <= max_abs and mn <= mean_abs, f"{what}: max {mx:.3e} mean {mn:.3e}"
+
+
+def _meta(T, P, W, n, kfi, off=0, rank=0, world=1, guards=None):
+    return lv.LVSAMetadata.build(total_latent_frames=T, num_patches=P, window_size=W, n_first_frames=n,
+                                 key_frame_interval=kfi, rank=rank, world=world, keyframe_offset=off,
+                                 boundary_guards=guards)
+
+
+SMALL = [
+    # T, P, W, n, kfi, off, H, Hkv, D, n_txt, dtype
+    (9, 256, 1, 1, 4, 3, 2, 2, 128, 0, torch.bfloat16),
+    (9, 256, 1, 1, 4, 3, 2, 2, 64, 0, torch.bfloat16),
+    (10, 4, 0, 2, 3, 0, 2, 2, 128, 0, torch.bfloat16),       # W=0, tiny frames -> generic masks
+    (21, 30, 3, 3, 4, 2, 4, 1, 128, 0, torch.bfloat16),      # GQA 4:1, frames < block
+    (9, 200, 1, 1, 4, 1, 4, 4, 128, 37, torch.bfloat16),     # text keys + text queries
+    (13, 150, 1, 1, 4, 0, 3, 3, 64, 26, torch.float16),      # fp16, D=64, text
+    (24, 130, 2, 1, 8, 5, 2, 2, 128, 0, torch.bfloat16),
+    (6, 8, 2, 1, 1, 0, 8, 2, 128, 16, torch.bfloat16),       # kfi=1: dense
+    (5, 30, 10, 1, None, 0, 2, 2, 64, 0, torch.bfloat16),    # W > T: dense
+    (1, 77, 0, 1, None, 0, 2, 2, 128, 3, torch.bfloat16),    # single frame
+    (17, 129, 2, 2, 5, 4, 2, 2, 128, 129, torch.float16),    # odd sizes, text tail
+]
+
+
+@pytest.mark.parametrize("cfg", SMALL, ids=[str(c[:10]) for c in SMALL])
+def test_fused_attention_small(cfg, gpu):
+    T, P, W, n, kfi, off, H, Hkv, D, n_txt, dt = cfg
+    N = T * P
+    m = _meta(T, P, W, n, kfi, off)
+    q, k, v, qt, kt, vt = _draw([(1, N, H, D), (1, N, Hkv, D), (1, N, Hkv, D), (1, n_txt, H, D),
+                                 (1, n_txt, Hkv, D), (1, n_txt, Hkv, D)], dtype=dt)
+    ref_rows = [set(r) for r in om.build_frame_mask(T, P, W, n, kfi, offset=off).rows]
+    args = dict(k_text=kt.to(gpu), v_text=vt.to(gpu), q_text=qt.to(gpu)) if n_txt else {}
+    res = lv.lvsa_attention(q.to(gpu), k.to(gpu), v.to(gpu), m, return_lse=True, **args)
+    ro, rl = oa.per_frame_sdpa(q.float(), k.float(), v.float(), ref_rows, P,
+                               k_extra=kt.float() if n_txt else None, v_extra=vt.float() if n_txt else None)
+    if n_txt:
+        o, ot, lse, lse_t = res
+        rto, rtl = oa.text_row_attention(qt.float(), k.float(), v.float(), kt.float(), vt.float())
+        _close(ot, rto, "text rows")
+        torch.testing.assert_close(lse_t.cpu(), rtl, atol=2e-2, rtol=0)
+    else:
+        o, lse = res
+    assert o.dtype == dt and o.shape == q.shape
+    _close(o, ro, "video rows")
+    torch.testing.assert_close(lse.cpu(), rl, atol=2e-2, rtol=0)
+
+
+def test_repeat_call_is_bitwise_identical(gpu):
+    T, P, H, D = 12, 300, 4, 128
+    m = _meta(T, P, 2, 1, 4, 1)
+    q, k, v = (x.to(gpu) for x in _draw([(1, T * P, H, D)] * 3))
+    a = lv.lvsa_attention(q, k, v, m)
+    b = lv.lvsa_attention(q, k, v, m)
+    assert torch.equal(a, b)
+
+
+def test_lvsa_sdpa_with_k_global_and_text(gpu):
+    # The reference call path: build_global_kv + text appended -> lvsa_sdpa.
+    T, P, W, H, Hkv, D, n_txt = 11, 160, 2, 4, 2, 128, 40
+    m = _meta(T, P, W, 1, 4, 2)
+    q, k, v, kt, vt = (x.to(gpu) for x in _draw([(1, T * P, H, D), (1, T * P, Hkv, D), (1, T * P, Hkv, D),
+                                                 (1, n_txt, Hkv, D), (1, n_txt, Hkv, D)]))
+    kg, vg = lv.build_global_kv(k, v, m.global_indices, P)
+    kg, vg = torch.cat([kg, kt], 1), torch.cat([vg, vt], 1)
+    out = lv.lvsa_sdpa(q, k, v, kg, vg, m)
+    out2 = lv.sparse_windowed_attention(q, k, v, kg, vg, m, backend="sdpa")
+    assert torch.equal(out, out2)
+    ref = om.build_frame_mask(T, P, W, 1, 4, offset=2)
+    ro, _ = oa.per_frame_sdpa(q.float(), k.float(), v.float(), om.window_only_relation(ref), P,
+                              k_extra=kg.float(), v_extra=vg.float())
+    _close(out, ro, "lvsa_sdpa")
+    fused = lv.lvsa_attention(q, k, v, m, k_text=kt, v_text=vt)
+    _close(fused, ro, "fused vs lvsa_sdpa reference")
+
+
+def test_lvsa_sdpa_context_parallel_shard(gpu):
+    # rank 1 of 2: local queries/keys, globals assembled from the full sequence.
+    T, P, W, H, D, world, rank = 12, 50, 2, 2, 128, 2, 1
+    guards = lv.compute_boundary_guard_frames(T, T * P // world, P, world, W)
+    m = _meta(T, P, W, 1, 5, 3, rank=rank, world=world, guards=guards)
+    q, k, v = _draw([(1, T * P, H, D)] * 3)
+    s, e = m.global_token_start, m.global_token_start + m.local_seq
+    kg = torch.cat([k[:, g * P:(g + 1) * P] for g in m.global_indices], 1)
+    vg = torch.cat([v[:, g * P:(g + 1) * P] for g in m.global_indices], 1)
+    out = lv.lvsa_sdpa(q[:, s:e].to(gpu), k[:, s:e].to(gpu), v[:, s:e].to(gpu), kg.to(gpu), vg.to(gpu), m)
+    # Oracle: the reference loop over local frames (lvsa/sparse_attention.py:674-704).
+    ref = torch.full((1, m.local_seq, H, D), float("nan"))
+    for f, qs, qe in m.local_frames:
+        parts_k = [kg.float()] + [k[:, s + a:s + b].float() for a, b in m.window_ctx[f]]
+        parts_v = [vg.float()] + [v[:, s + a:s + b].float() for a, b in m.window_ctx[f]]
+        o, _ = oa.dense_attention(q[:, s + qs:s + qe].float(), torch.cat(parts_k, 1), torch.cat(parts_v, 1))
+        ref[:, qs:qe] = o
+    _close(out, ref, "cp shard")
+
+
+def test_flashinfer_backend_and_wrapper(gpu):
+    T, P, W, H, D = 9, 96, 1, 4, 128
+    m = _meta(T, P, W, 1, 4, 3)
+    m.ensure_device(gpu)
+    q, k, v = (x.to(gpu) for x in _draw([(1, T * P, H, D)] * 3))
+    kg, vg = lv.build_global_kv(k, v, m.global_indices, P)
+    ck = q.new_zeros(1, m.fi_N, H, D)
+    cv = q.new_zeros(1, m.fi_N, H, D)
+    for src, dst in m.fi_global_copies:
+        ck[:, dst:dst + P], cv[:, dst:dst + P] = kg[:, src:src + P], vg[:, src:src + P]
+    for src, dst in m.fi_local_copies:
+        ck[:, dst:dst + P], cv[:, dst:dst + P] = k[:, src:src + P], v[:, src:src + P]
+    w = lv.BlockSparseAttentionWrapper(torch.empty(1, dtype=torch.uint8, device=gpu))
+    w.plan(m.fi_indptr, m.fi_indices, M=m.fi_M, N=m.fi_N, R=P, C=P, num_qo_heads=H, num_kv_heads=H,
+           head_dim=D, q_data_type="bfloat16")
+    out = lv.sparse_windowed_attention(q, k, v, kg, vg, m, backend="flashinfer", k_compact=ck, v_compact=cv,
+                                       fi_wrapper=w)
+    rows = [set(r) for r in om.build_frame_mask(T, P, W, 1, 4, offset=3).rows]
+    ro, rl = oa.per_frame_sdpa(q.float(), k.float(), v.float(), rows, P)
+    _close(out, ro, "flashinfer backend")
+    o2, lse2 = w.run(q[0], ck[0], cv[0], return_lse=True)
+    torch.testing.assert_close(lse2.cpu(), (rl[0].transpose(0, 1) / math.log(2.0)).cpu(), atol=3e-2, rtol=0)
+
+
+def test_dual_stream_runner_gqa(gpu):
+    # lvsa-vllm-omni/tests/test_flashinfer_runner.py: H=8, Hkv=2, D=128, P=8, 16 und tokens.
+    H, HKV, D, P, S_UND = 8, 2, 128, 8, 16
+    for T_lat, ref_frames, kfi in [(24, 6, None), (6, 6, 1)]:
+        if kfi is None:
+            kfi = lv.compute_auto_kfi(T_lat, 2, 1, reference_frames=ref_frames)
+        m = lv.LVSAMetadata.build(total_latent_frames=T_lat, num_patches=P, window_size=2, n_first_frames=1,
+                                  key_frame_interval=kfi, rank=0, world=1, reference_frames=ref_frames)
+        q, k, v, ku, vu = (x.to(gpu) for x in _draw([(1, T_lat * P, H, D), (1, T_lat * P, HKV, D),
+                                                     (1, T_lat * P, HKV, D), (1, S_UND, HKV, D),
+                                                     (1, S_UND, HKV, D)], seed=T_lat))
+        kg, vg = lv.build_global_kv(k, v, m.global_indices, P)
+        kg, vg = torch.cat([kg, ku], 1), torch.cat([vg, vu], 1)
+        out = lv.get_shared_runner().run(q, k, v, kg, vg, m)
+        assert out.shape == q.shape and torch.isfinite(out.float()).all()
+        rows = [set(r) for r in om.build_frame_mask(T_lat, P, 2, 1, kfi).rows]
+        ro, _ = oa.per_frame_sdpa(q.float(), k.float(), v.float(), rows, P, k_extra=ku.float(), v_extra=vu.float())
+        _close(out, ro, f"runner T={T_lat}")
+        if kfi == 1:
+            dense, _ = oa.dense_attention(q.float(), torch.cat([k, ku], 1).float(), torch.cat([v, vu], 1).float())
+            rel = ((out.float() - dense).norm() / dense.norm()).item()
+            assert rel < 2e-2
+
+
+def test_build_global_kv_exact(gpu):
+    # lvsa-vllm-omni/tests/test_global_kv.py
+    B, T, P, H, D = 1, 5, 2, 1, 8
+    k = torch.arange(T * P, dtype=torch.float32).view(1, T * P, 1, 1).expand(B, T * P, H, D).contiguous().to(gpu)
+    kg, _ = lv.build_global_kv(k, k.clone(), [1, 3], P)
+    assert kg[0, :, 0, 0].tolist() == [2, 3, 6, 7]
+    kb = torch.randn(3, 8 * 4, 2, 8, device=gpu, dtype=torch.bfloat16)
+    kg, vg = lv.build_global_kv(kb, kb, [0, 4], 4)
+    for b in range(3):
+        assert torch.equal(kg[b, :4], kb[b, :4]) and torch.equal(kg[b, 4:], kb[b, 16:20])
+    e, _ = lv.build_global_kv(kb, kb, [], 4)
+    assert e.shape == (3, 0, 2, 8)
+    full, _ = lv.build_global_kv(kb, kb, list(range(8)), 4)
+    assert torch.equal(full, kb)
+
+
+def test_single_prefill_dense(gpu):
+    q, k, v = (x.to(gpu) for x in _draw([(1, 70, 4, 128), (1, 333, 2, 128), (1, 333, 2, 128)]))
+    o, lse = lv.single_prefill_with_kv_cache(q[0], k[0], v[0], causal=False, return_lse=True)
+    ro, rl = oa.dense_attention(q.float(), k.float(), v.float())
+    _close(o.unsqueeze(0), ro, "single_prefill")
+    torch.testing.assert_close(lse.cpu(), rl[0].transpose(0, 1).cpu() / math.log(2.0), atol=3e-2, rtol=0)
+
+
+def test_batch_views_and_fp32_inputs(gpu):
+    T, P, W, H, D = 8, 64, 1, 2, 64
+    m = _meta(T, P, W, 1, 3, 1)
+    qkv = torch.randn(2, T * P, 3 * H * D, device=gpu, dtype=torch.bfloat16)
+    q, k, v = (t.unflatten(-1, (H, D)) for t in qkv.chunk(3, dim=-1))   # strided views
+    out = lv.lvsa_attention(q, k, v, m)
+    rows = [set(r) for r in om.build_frame_mask(T, P, W, 1, 3, offset=1).rows]
+    for b in range(2):
+        ro, _ = oa.per_frame_sdpa(q[b:b + 1].float(), k[b:b + 1].float(), v[b:b + 1].float(), rows, P)
+        _close(out[b:b + 1], ro, f"batch {b}")
+    out32 = lv.lvsa_attention(q.float(), k.float(), v.float(), m)
+    assert out32.dtype == torch.float32
+    _close(out32, out.float(), "fp32 inputs", max_abs=1e-6, mean_abs=1e-7)
+
+
+def test_rejects_unsupported_head_dim(gpu):
+    m = _meta(4, 16, 1, 1, 2)
+    q = torch.randn(1, 64, 2, 96, device=gpu, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="head_dim 96"):
+        lv.lvsa_attention(q, q, q, m)
+
+
+# ── BASELINE shapes at full size ─────────────────────────────────────────────
+
+BASELINE = [
+    # name, T, P, W, kfi, off, H, D, n_txt, dtype, spot frames
+    ("cpu", 9, 256, 1, 4, 3, 12, 128, 0, torch.float32, None),
+    ("wan4x_off0", 84, 1560, 2, 8, 0, 12, 128, 0, torch.bfloat16, [0, 1, 41, 42, 82, 83]),
+    ("wan4x_off5", 84, 1560, 2, 8, 5, 12, 128, 0, torch.bfloat16, [1, 13, 50, 83]),
+    ("wan6x_w1", 121, 1560, 1, 8, 3, 12, 128, 0, torch.bfloat16, [0, 60, 120]),
+    ("cog", 13, 1350, 1, 4, 0, 48, 64, 226, torch.bfloat16, [0, 5, 12]),
+    ("hv_off2", 49, 1590, 2, 8, 2, 16, 128, 256, torch.bfloat16, [0, 24, 48]),
+]
+
+
+@pytest.mark.parametrize("cfg", BASELINE, ids=[c[0] for c in BASELINE])
+def test_baseline_config_parity(cfg, gpu):
+    name, T, P, W, kfi, off, H, D, n_txt, dt, frames = cfg
+    N = T * P
+    q, k, v, qt, kt, vt = _draw([(1, N, H, D), (1, N, H, D), (1, N, H, D), (1, n_txt, H, D),
+                                 (1, n_txt, H, D), (1, n_txt, H, D)], dtype=dt)
+    qd, kd, vd = q.to(gpu), k.to(gpu), v.to(gpu)
+    m = _meta(T, P, W, 1, kfi, off)
+    if n_txt:
+        o, ot = lv.lvsa_attention(qd, kd, vd, m, k_text=kt.to(gpu), v_text=vt.to(gpu), q_text=qt.to(gpu))
+    else:
+        o = lv.lvsa_attention(qd, kd, vd, m)
+    # size-independent properties: finite, convex combination of value rows
+    vmax = v.abs().max().item() if not n_txt else max(v.abs().max().item(), vt.abs().max().item())
+    assert torch.isfinite(o.float()).all()
+    assert o.float().abs().max().item() <= vmax * 1.01
+    rows = [set(r) for r in om.build_frame_mask(T, P, W, 1, kfi, offset=off).rows]
+    ro, _ = oa.per_frame_sdpa(qd.float(), kd.float(), vd.float(), rows, P,
+                              k_extra=kt.to(gpu).float() if n_txt else None,
+                              v_extra=vt.to(gpu).float() if n_txt else None, frames=frames)
+    _close(o, ro, name)
+    if n_txt:
+        rto, _ = oa.text_row_attention(qt.to(gpu).float(), kd.float(), vd.float(), kt.to(gpu).float(),
+                                       vt.to(gpu).float())
+        _close(ot, rto, name + " text rows")

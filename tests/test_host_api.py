@@ -1,0 +1,140 @@
+"""Host-side API of the package (CPU only): helpers and LVSAMetadata host
+fields against the golden vectors; the reference's own unit-test contracts;
+error behaviour; no CPU compute path."""
+
+import io
+
+import pytest
+import torch
+
+import longvideosparseattention_amd as lv
+from longvideosparseattention_amd import sparse_attention as sa
+
+
+def _meta(a):
+    return sa.LVSAMetadata.build(
+        total_latent_frames=a["T"], num_patches=a["P"], window_size=a["W"], n_first_frames=a["n_first"],
+        key_frame_interval=a["kfi"], rank=a["rank"], world=a["world"], expand_window=a["expand"],
+        keyframe_offset=a["offset"], boundary_guards=a["guards"])
+
+
+def test_helpers_match_golden(golden):
+    for rec in golden["windows"]:
+        G = set(rec["G"])
+        assert list(sa.get_window_bounds(rec["f"], rec["W"], rec["T"], rec["expand"], G, len(G))) == rec["bounds"]
+    for rec in golden["auto_kfi"]:
+        assert sa.compute_auto_kfi(rec["T"], rec["W"], rec["n_first"], reference_frames=rec["ref"],
+                                   sparsity_scale=rec["scale"]) == rec["kfi"]
+
+
+def test_metadata_host_fields_match_golden(golden):
+    for rec in golden["random"] + golden["baseline"]:
+        a = rec["args"]
+        m = _meta(a)
+        tag = str(a)
+        assert m.global_indices == rec["global_indices"], tag
+        assert m.window_bounds.tolist() == rec["window_bounds"], tag
+        assert (m.fi_M, m.fi_N, m.fi_MB, m.fi_compact_n) == (rec["fi_M"], rec["fi_N"], rec["fi_MB"],
+                                                             rec["fi_compact_n"]), tag
+        assert m.fi_nnz == rec["fi_indptr"][-1], tag
+        assert (m.local_seq, m.global_token_start) == (rec["local_seq"], rec["global_token_start"]), tag
+        if "local_frames" in rec:
+            assert [list(x) for x in m.local_frames] == rec["local_frames"], tag
+            assert {str(k): [list(p) for p in v] for k, v in m.window_ctx.items()} == rec["window_ctx"], tag
+            assert m.attended_indices.tolist() == rec["attended_indices"], tag
+            assert m.attended_C == rec["attended_C"], tag
+            assert [list(x) for x in m.fi_global_copies] == rec["fi_global_copies"], tag
+            assert [list(x) for x in m.fi_local_copies] == rec["fi_local_copies"], tag
+            assert m.global_frame_mask.tolist() == rec["global_frame_mask"], tag
+
+
+# Contracts of tests/test_sparse_attention.py:22-133 (host fields only).
+class TestLVSAMetadataBuild:
+    def _build(self, T=21, P=30, W=3, n_first=1, kfi=4, rank=0, world=1, expand=True):
+        return lv.LVSAMetadata.build(total_latent_frames=T, num_patches=P, window_size=W, n_first_frames=n_first,
+                                     key_frame_interval=kfi, rank=rank, world=world, expand_window=expand)
+
+    def test_basic_build(self):
+        m = self._build()
+        assert (m.total_latent_frames, m.num_patches, m.local_seq, m.global_token_start) == (21, 30, 630, 0)
+
+    def test_local_frames_cover_local_seq(self):
+        m = self._build()
+        assert sum(e - s for _, s, e in m.local_frames) == m.local_seq
+
+    def test_window_ctx_excludes_globals(self):
+        m = self._build()
+        for f, parts in m.window_ctx.items():
+            for s, e in parts:
+                for t in range(s, e, m.num_patches):
+                    assert (m.global_token_start + t) // m.num_patches not in m.global_set
+
+    def test_tables(self):
+        m = self._build()
+        assert m.global_frame_mask.shape == (21,) and m.window_bounds.shape == (21, 2)
+        assert m.attended_indices.shape == (len(m.local_frames), m.attended_C)
+        assert len(m.fi_global_copies) + len(m.fi_local_copies) == m.fi_compact_n
+        assert m.global_src_idx.numel() == len(m.global_indices) * 30
+        assert torch.equal(m.global_dst_idx[:30], torch.arange(30))
+
+    def test_multi_gpu_rank1(self):
+        m = self._build(rank=1, world=2)
+        assert m.global_token_start == m.local_seq == 21 * 30 // 2
+
+    def test_indivisible_world_asserts(self):
+        with pytest.raises(AssertionError, match="must be divisible by world"):
+            self._build(T=5, P=3, world=2)
+
+    def test_boundary_guards_and_rotation(self):
+        m = lv.LVSAMetadata.build(total_latent_frames=21, num_patches=30, window_size=3, n_first_frames=1,
+                                  key_frame_interval=4, rank=0, world=1, boundary_guards=[5, 10, 15])
+        assert {5, 10, 15} <= m.global_set
+        m0 = self._build()
+        m1 = lv.LVSAMetadata.build(total_latent_frames=21, num_patches=30, window_size=3, n_first_frames=1,
+                                   key_frame_interval=4, rank=0, world=1, keyframe_offset=1)
+        assert m0.global_indices != m1.global_indices
+        assert len(m0.global_indices) == len(m1.global_indices)
+
+    def test_kfi_used_verbatim(self):
+        # tests/test_sparse_attention.py:590-611
+        m = lv.LVSAMetadata.build(total_latent_frames=33, num_patches=30, window_size=3, n_first_frames=1,
+                                  key_frame_interval=1, rank=0, world=1, reference_frames=33)
+        assert m.key_frame_interval == 1 and len(m.global_set) == 33
+
+    def test_ensure_device_cpu_is_noop(self):
+        m = self._build()
+        m.ensure_device(torch.device("cpu"))
+
+
+def test_flashinfer_backend_requires_buffers():
+    # tests/test_sparse_attention.py:284-292
+    m = lv.LVSAMetadata.build(total_latent_frames=5, num_patches=4, window_size=1, n_first_frames=1,
+                              key_frame_interval=None, rank=0, world=1)
+    q = k = v = kg = vg = torch.randn(1, 20, 2, 8)
+    with pytest.raises(AssertionError, match="FlashInfer backend requires"):
+        lv.sparse_windowed_attention(q, k, v, kg, vg, m, backend="flashinfer")
+
+
+def test_no_cpu_compute_path():
+    m = lv.LVSAMetadata.build(total_latent_frames=5, num_patches=4, window_size=1, n_first_frames=1,
+                              key_frame_interval=None, rank=0, world=1)
+    q = torch.randn(1, 20, 2, 64)
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        lv.lvsa_sdpa(q, q, q, q[:, :4], q[:, :4], m)
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        lv.lvsa_attention(q, q, q, m)
+
+
+def test_print_mask_compact():
+    buf = io.StringIO()
+    sa.print_attention_mask_compact(10, 2, {0, 3, 6, 9}, True, file=buf)
+    lines = buf.getvalue().splitlines()
+    assert len(lines) == 12 and "G=global" in lines[-1]
+    assert lines[1].startswith("0 |") and lines[1].endswith(f"| {len(lines[1].split('|')[1]) - lines[1].split('|')[1].count('.')}")
+
+
+def test_lazy_exports():
+    for name in lv.__all__:
+        assert getattr(lv, name) is not None
+    with pytest.raises(AttributeError):
+        lv.does_not_exist

@@ -1,0 +1,266 @@
+"""Pin the CPU mask oracle (CPU only).
+
+Three independent kinds of evidence:
+1. golden vectors written from the reference implementation itself
+   (tests/golden/make_golden.py) — exact window tie-breaks, CSR contents,
+   compact numbering, copy lists, context-parallel ranks;
+2. the known answers held by the reference's own tests
+   (tests/test_swa_processor.py, tests/test_sparse_attention.py);
+3. brute-force characterisations (dense token masks, window invariants).
+"""
+
+import itertools
+import random
+
+import numpy as np
+import pytest
+
+from oracle import lvsa_mask as om
+
+
+def _build(rec_args):
+    a = rec_args
+    return om.build_frame_mask(a["T"], a["P"], a["W"], a["n_first"], a["kfi"], rank=a["rank"],
+                               world=a["world"], expand=a["expand"], offset=a["offset"], guards=a["guards"])
+
+
+# ── 1. golden vectors ────────────────────────────────────────────────────────
+
+
+def test_golden_baseline_csr(golden):
+    assert len(golden["baseline"]) == 45
+    for rec in golden["baseline"]:
+        m = _build(rec["args"])
+        assert m.global_indices == rec["global_indices"], rec["name"]
+        assert [list(b) for b in m.window_bounds] == rec["window_bounds"], rec["name"]
+        assert m.indptr == rec["fi_indptr"], rec["name"]
+        assert m.indices == rec["fi_indices"], rec["name"]
+        assert (m.MB, m.compact_n) == (rec["fi_MB"], rec["fi_compact_n"])
+
+
+def test_golden_random_metadata(golden):
+    recs = golden["random"]
+    assert len(recs) >= 300 and any(r["args"]["world"] > 1 for r in recs)
+    for rec in recs:
+        a = rec["args"]
+        m = _build(a)
+        tag = str(a)
+        assert m.global_indices == rec["global_indices"], tag
+        assert [list(b) for b in m.window_bounds] == rec["window_bounds"], tag
+        assert m.indptr == rec["fi_indptr"], tag
+        assert m.indices == rec["fi_indices"], tag
+        assert m.MB * a["P"] == rec["fi_M"] and m.compact_n * a["P"] == rec["fi_N"], tag
+        assert (m.local_seq, m.gts) == (rec["local_seq"], rec["global_token_start"]), tag
+        assert [list(x) for x in m.local_frames] == rec["local_frames"], tag
+        assert {str(k): [list(p) for p in v] for k, v in m.window_ctx.items()} == rec["window_ctx"], tag
+        C = max(len(r) for r in m.attended_rows)
+        padded = [r + [r[-1]] * (C - len(r)) for r in m.attended_rows]
+        assert padded == rec["attended_indices"] and C == rec["attended_C"], tag
+        assert [list(x) for x in m.global_copies] == rec["fi_global_copies"], tag
+        assert [list(x) for x in m.local_copies] == rec["fi_local_copies"], tag
+        gm = [1 if f in m.global_set else 0 for f in range(a["T"])]
+        assert gm == rec["global_frame_mask"], tag
+
+
+def test_golden_window_bounds_arbitrary_global_sets(golden):
+    for rec in golden["windows"]:
+        G = set(rec["G"])
+        got = om.get_window_bounds(rec["f"], rec["W"], rec["T"], rec["expand"], G, len(G))
+        assert list(got) == rec["bounds"], rec
+
+
+def test_golden_auto_kfi(golden):
+    for rec in golden["auto_kfi"]:
+        got = om.compute_auto_kfi(rec["T"], rec["W"], rec["n_first"], reference_frames=rec["ref"],
+                                  sparsity_scale=rec["scale"])
+        assert got == rec["kfi"], rec
+
+
+# ── 2. known answers of the reference's own tests ────────────────────────────
+
+
+def test_adaptive_known_answers():
+    # tests/test_swa_processor.py:18-57
+    assert om.adaptive_window_bounds(10, 3, 21) == (7, 13)
+    lo, hi = om.adaptive_window_bounds(0, 3, 21)
+    assert lo == 0 and hi >= 6
+    lo, hi = om.adaptive_window_bounds(20, 3, 21)
+    assert hi == 20 and lo <= 14
+    for f in range(21):
+        lo, hi = om.adaptive_window_bounds(f, 3, 21)
+        assert hi - lo + 1 == 7
+    for f in range(8):
+        assert om.adaptive_window_bounds(f, 5, 8) == (0, 7)
+    for f in range(50):
+        lo, hi = om.adaptive_window_bounds(f, 4, 50)
+        assert lo <= f <= hi
+
+
+def test_global_indices_known_answers():
+    # tests/test_swa_processor.py:113-184
+    assert all(f in om.compute_global_indices(21, 3, 5, 0) for f in (0, 1, 2))
+    assert set(om.compute_global_indices(21, 1, 5, 0)) >= {0, 5, 10, 15, 20}
+    assert om.compute_global_indices(21, 1, 5, 2) == [0, 1, 2, 7, 12, 17]
+    assert om.compute_global_indices(21, 3, None, 0) == [0, 1, 2]
+    covered = set()
+    for off in range(4):
+        covered |= set(om.compute_global_indices(21, 1, 4, off))
+    assert covered == set(range(21))
+    # SURVEY worked examples: CPU config and Wan 4x step 5 (85 mod 84 = 1).
+    assert om.compute_global_indices(9, 1, 4, 3) == [0, 2, 3, 7]
+    assert om.compute_global_indices(84, 1, 8, 5) == [0, 1, 5, 13, 21, 29, 37, 45, 53, 61, 69, 77]
+    assert om.compute_global_indices(13, 1, 4, 0) == [0, 4, 8, 12]
+
+
+def test_boundary_guard_known_answers():
+    # tests/test_swa_processor.py:63-104
+    assert om.compute_boundary_guard_frames(21, 21 * 30, 30, 1, 3) == []
+    assert om.compute_boundary_guard_frames(20, 100, 10, 2, 2) == [8, 9, 10, 11, 12]
+
+
+def test_auto_kfi_known_answers():
+    # tests/test_sparse_attention.py:426-441 (kfi = 1 at T <= reference)
+    for T, ref in [(21, 21), (20, 21), (17, 33), (33, 33), (1, 21)]:
+        assert om.compute_auto_kfi(T, 12, 8, reference_frames=ref) == 1
+    for T, ref in [(49, 33), (65, 33), (81, 21)]:
+        kfi = om.compute_auto_kfi(T, 12, 8, reference_frames=ref)
+        assert len(om.compute_global_indices(T, 8, kfi)) < T
+
+
+def test_cpu_config_frame_rows():
+    # frame 1 attends {0,1,2,3,4,5,7}, not the naive {0,1,2,3,7}.
+    m = om.build_frame_mask(9, 256, 1, 1, 4, offset=3)
+    assert m.rows[1] == [0, 1, 2, 3, 4, 5, 7]
+    assert all(len(r) == 7 for r in m.rows)
+    assert m.indptr[-1] == 63
+
+
+def test_csr_edge_cases():
+    # tests/test_swa_processor.py:618-740
+    m = om.build_frame_mask(1, 4, 0, 1, None)
+    assert m.compact_n == 1 and m.indptr[-1] == 1
+    m = om.build_frame_mask(8, 4, 0, 1, 1)
+    assert m.compact_n == 8 and m.local_copies == []
+    m = om.build_frame_mask(10, 4, 0, 2, 3)
+    assert m.compact_n == len(m.global_indices)
+    assert all(m.indptr[i + 1] - m.indptr[i] == len(m.global_indices) for i in range(m.MB))
+    m = om.build_frame_mask(21, 30, 3, 3, 4)
+    for i in range(m.MB):
+        row = m.indices[m.indptr[i]:m.indptr[i + 1]]
+        assert row == sorted(row) and len(row) >= len(m.global_indices)
+    m = om.build_frame_mask(5, 30, 10, 1, None)
+    assert all(b == (0, 4) for b in m.window_bounds)
+
+
+# ── 3. brute force ───────────────────────────────────────────────────────────
+
+
+def _window_brute(f, W, T, G, expand):
+    """Characterise the expanded window without simulating the loop.
+
+    The expansion pushes left then right alternately; after k_l left and k_r
+    right pushes (k_l - k_r in {0, 1} while both sides are open) the window is
+    [lo0 - k_l, hi0 + k_r].  Enumerate all pairs (k_l, k_r) that respect the
+    alternation, ordered by the number of pushes, and return the first whose
+    window holds enough non-global frames (or the whole sequence).
+    """
+    if W == 0:
+        return f, f - 1
+    lo0 = max(0, min(f - W, T - 1 - 2 * W))
+    hi0 = min(T - 1, max(f + W, 2 * W))
+    if not expand:
+        return lo0, hi0
+    need = min(2 * W + 1, T - len(G))
+    nl, nr = lo0, T - 1 - hi0          # pushes available on each side
+
+    def pushes(n):
+        # n-th state of the L,R,L,R,... sequence with exhausted sides skipped
+        seq = []
+        l = r = 0
+        while len(seq) < n:
+            if l < nl:
+                l += 1
+                seq.append(("L", l, r))
+                if len(seq) == n:
+                    break
+            if r < nr:
+                r += 1
+                seq.append(("R", l, r))
+            if l >= nl and r >= nr:
+                break
+        return seq[n - 1][1:] if n else (0, 0)
+
+    for n in range(0, nl + nr + 1):
+        l, r = pushes(n)
+        lo, hi = lo0 - l, hi0 + r
+        if sum(1 for x in range(lo, hi + 1) if x not in G) >= need:
+            return lo, hi
+    return 0, T - 1
+
+
+def test_expanded_window_matches_brute_force():
+    rng = random.Random(7)
+    for _ in range(3000):
+        T = rng.randint(1, 45)
+        W = rng.randint(0, 6)
+        G = set(rng.sample(range(T), rng.randint(0, T)))
+        f = rng.randrange(T)
+        expand = rng.random() < 0.9
+        assert om.get_window_bounds(f, W, T, expand, G, len(G)) == _window_brute(f, W, T, G, expand)
+
+
+def test_window_invariants_over_keyframe_patterns():
+    # tests/test_swa_processor.py:374-412 and tests/test_sparse_attention.py:516-588
+    for T, W, n, kfi, off in itertools.product([7, 21, 41, 84], [1, 2, 3], [1, 3], [4, 8], [0, 1, 3]):
+        G = om.compute_global_indices(T, n, kfi, off)
+        Gs = set(G)
+        target = min(2 * W + 1, T - len(G))
+        for f in range(T):
+            lo, hi = om.expanded_window_bounds(f, W, T, Gs, len(G))
+            assert 0 <= lo <= f <= hi < T
+            non_global = sum(1 for x in range(lo, hi + 1) if x not in Gs)
+            assert non_global >= target or (lo == 0 and hi == T - 1)
+            assert len(Gs | set(range(lo, hi + 1))) == len(G) + min(2 * W + 1, T - len(G))
+
+
+def test_block_csr_matches_dense_token_mask():
+    rng = random.Random(3)
+    for _ in range(25):
+        T, P = rng.randint(1, 12), rng.randint(1, 40)
+        m = om.build_frame_mask(T, P, rng.randint(0, 3), rng.randint(0, 2), rng.choice([None, 2, 3, 5]),
+                                offset=rng.randint(0, 4))
+        rel = om.frame_relation(m)
+        N = T * P
+        tm = om.token_mask(rel, P, N, N)
+        bq, bk = rng.choice([4, 16, 64, 128]), rng.choice([4, 16, 64])
+        indptr, cols = om.block_csr(rel, P, N, N, bq, bk)
+        for i in range(-(-N // bq)):
+            blk = tm[i * bq:(i + 1) * bq]
+            want = [j for j in range(-(-N // bk)) if blk[:, j * bk:(j + 1) * bk].any()]
+            assert cols[indptr[i]:indptr[i + 1]] == want
+
+
+def test_block_flops_against_token_mask():
+    m = om.build_frame_mask(9, 256, 1, 1, 4, offset=3)
+    rel = om.frame_relation(m)
+    N = 9 * 256
+    tm = om.token_mask(rel, 256, N, N)
+    fb, fx = om.block_flops(rel, 256, N, 64, 64, 12, 128)
+    assert fx == 4 * 12 * 128 * int(tm.sum())
+    blocks = tm.reshape(N // 64, 64, N // 64, 64).any(axis=(1, 3))
+    assert fb == 4 * 12 * 128 * int(blocks.sum()) * 64 * 64
+    assert abs(fb / 1e9 - 25.4) < 0.1   # 25.4 GFLOP
+
+
+def test_token_mask_semantics_small():
+    # Frame rule written directly on tokens, independent of the CSR code path.
+    T, P, W, n, kfi, off = 9, 3, 1, 1, 4, 3
+    G = set(om.compute_global_indices(T, n, kfi, off))
+    m = om.build_frame_mask(T, P, W, n, kfi, offset=off)
+    tm = om.token_mask(om.frame_relation(m), P, T * P, T * P)
+    for i in range(T * P):
+        f = i // P
+        lo, hi = om.get_window_bounds(f, W, T, True, G, len(G))
+        for j in range(T * P):
+            g = j // P
+            assert tm[i, j] == (g in G or lo <= g <= hi)
