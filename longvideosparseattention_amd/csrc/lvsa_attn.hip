@@ -181,41 +181,63 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
   }
   const int e0 = p.tile_indptr[tile], e1 = p.tile_indptr[tile + 1];
 
+  // Key sources: 0 = frame-structured key/value, 1 = dense extra rows.
   const char* kb0 = p.k + 2 * (batch * p.k_str[0] + hk * p.k_str[2]);
   const char* vb0 = p.v + 2 * (batch * p.v_str[0] + hk * p.v_str[2]);
   const char* kb1 = p.n_x ? p.kx + 2 * (batch * p.kx_str[0] + hk * p.kx_str[2]) : kb0;
   const char* vb1 = p.n_x ? p.vx + 2 * (batch * p.vx_str[0] + hk * p.vx_str[2]) : vb0;
-  const int64_t krs0 = 2 * p.k_str[1], vrs0 = 2 * p.v_str[1];
-  const int64_t krs1 = 2 * p.kx_str[1], vrs1 = 2 * p.vx_str[1];
+  const uint32_t krs0 = (uint32_t)(2 * p.k_str[1]), vrs0 = (uint32_t)(2 * p.v_str[1]);
+  const uint32_t krs1 = (uint32_t)(2 * p.kx_str[1]), vrs1 = (uint32_t)(2 * p.vx_str[1]);
 
   // Per-lane DMA geometry: instruction ii of this wave covers LDS bytes
-  // [(wave*NIW + ii) KiB, +1 KiB); lane -> (row, logical chunk).
-  int dma_row[NIW], dma_chunk[NIW];
+  // [(wave*NIW + ii) KiB, +1 KiB); lane -> (row within the block, byte offset
+  // of the logical 16-byte chunk it fetches).
+  uint32_t dma_row[NIW], dma_cb[NIW];
 #pragma unroll
   for (int ii = 0; ii < NIW; ++ii) {
     const int pos = (wave * NIW + ii) * 64 + lane;
     const int r = pos / NCH, pc = pos % NCH;
-    dma_row[ii] = r;
-    dma_chunk[ii] = pc ^ swz<D>(r);
+    dma_row[ii] = (uint32_t)r;
+    dma_cb[ii] = (uint32_t)((pc ^ swz<D>(r)) * 16);
   }
 
-  auto issue = [&](int e, int stage) {
-    const uint2 ent = p.entries[e];
-    const bool extra = (ent.x >> 31) != 0;
-    const int64_t k0 = (int64_t)(ent.x & 0x7fffffffu) * kBN;
-    const char* kb = extra ? kb1 : kb0;
-    const char* vb = extra ? vb1 : vb0;
-    const int64_t krs = extra ? krs1 : krs0, vrs = extra ? vrs1 : vrs0;
+  // Plan entries of this tile, 64 at a time in a VGPR (lane i holds entry
+  // base + i); a uniform entry is read with v_readlane.  The next batch is
+  // prefetched one batch ahead so a batch switch never waits on memory.
+  uint32_t ec_x = 0, ec_y = 0, en_x = 0, en_y = 0;
+  int eb = e0;
+  {
+    const uint2* ents = p.entries;
+    if (e0 + lane < e1) {
+      const uint2 t = ents[e0 + lane];
+      ec_x = t.x;
+      ec_y = t.y;
+    }
+    if (e0 + 64 + lane < e1) {
+      const uint2 t = ents[e0 + 64 + lane];
+      en_x = t.x;
+      en_y = t.y;
+    }
+  }
+
+  auto issue = [&](uint32_t ex, int stage) {
+    const bool extra = (ex >> 31) != 0;
     const int64_t nsrc = extra ? p.n_x : p.n_k;
+    int64_t k0 = (int64_t)(ex & 0x7fffffffu) * kBN;
+    if (k0 >= nsrc) k0 = 0;  // never produced by the plan; keeps every DMA in bounds
+    const uint32_t krs = extra ? krs1 : krs0, vrs = extra ? vrs1 : vrs0;
+    const char* kb = (extra ? kb1 : kb0) + k0 * krs;
+    const char* vb = (extra ? vb1 : vb0) + k0 * vrs;
+    // rows past the end of the source re-read its last row (masked later)
+    const uint32_t lim = (uint32_t)((nsrc - 1 - k0) < (kBN - 1) ? (nsrc - 1 - k0) : (kBN - 1));
     lds_char* ks = smem + stage * STAGE;
     lds_char* vs = ks + TILE;
 #pragma unroll
     for (int ii = 0; ii < NIW; ++ii) {
-      int64_t key = k0 + dma_row[ii];
-      key = key < nsrc ? key : nsrc - 1;
+      const uint32_t r = dma_row[ii] < lim ? dma_row[ii] : lim;
       const int off = (wave * NIW + ii) * 1024;
-      dma16(kb + key * krs + dma_chunk[ii] * 16, ks + off);
-      dma16(vb + key * vrs + dma_chunk[ii] * 16, vs + off);
+      dma16(kb + (r * krs + dma_cb[ii]), ks + off);
+      dma16(vb + (r * vrs + dma_cb[ii]), vs + off);
     }
   };
 
@@ -255,13 +277,33 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
   const float cs = p.scale_log2;
   const int my_tile_row = 32 * wave + i32;
 
-  if (e0 < e1) issue(e0, 0);
+  uint32_t nx = 0, ny = 0;   // entry of the next block (uniform)
+  if (e0 < e1) {
+    nx = __builtin_amdgcn_readlane(ec_x, 0);
+    ny = __builtin_amdgcn_readlane(ec_y, 0);
+    issue(nx, 0);
+  }
   for (int e = e0; e < e1; ++e) {
     const int stage = (e - e0) & 1;
+    const uint32_t cx = nx, cy = ny;
     wait_vm0();
     __syncthreads();
-    if (e + 1 < e1) issue(e + 1, stage ^ 1);
-    const uint2 ent = p.entries[e];
+    if (e + 1 < e1) {
+      if (e + 1 - eb == 64) {
+        eb += 64;
+        ec_x = en_x;
+        ec_y = en_y;
+        en_x = en_y = 0;
+        if (eb + 64 + lane < e1) {
+          const uint2 t = p.entries[eb + 64 + lane];
+          en_x = t.x;
+          en_y = t.y;
+        }
+      }
+      nx = __builtin_amdgcn_readlane(ec_x, e + 1 - eb);
+      ny = __builtin_amdgcn_readlane(ec_y, e + 1 - eb);
+      issue(nx, stage ^ 1);
+    }
     const lds_char* ks = smem + stage * STAGE;
     const lds_char* vs = ks + TILE;
 
@@ -275,42 +317,47 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
       s1 = O::mfma(a1, qf[c], s1);
     }
 
-    // Masks.  Register r of sub-tile t holds key 32t + 8(r/4) + 4h + r%4.
-    const uint32_t desc = ent.y;
-    const uint32_t kind = desc & 3u;
-    if (kind == kKindTwoPart) {
-      const int bits = (desc >> 2) & 0xF;
-      const int kb = (int)((desc >> 8) & 0xFF) - 4 * h;
-      const int qs = (desc >> 16) & 0xFF;
-      const bool rb = my_tile_row >= qs;
-      const bool lo_ok = (bits >> (rb ? 2 : 0)) & 1;
-      const bool hi_ok = (bits >> (rb ? 3 : 1)) & 1;
+    // Masks.  Bit r of `keep` covers register r%16 of sub-tile r/16, which
+    // holds key 8q + j + 4h of the block with q = r/4, j = r%4.
+    const uint32_t kind = cy & 3u;
+    if (kind != kKindNone) {
+      uint32_t keep;
+      if (kind == kKindTwoPart) {
+        const int bits = (cy >> 2) & 0xF;
+        const int kb = (int)((cy >> 8) & 0xFF) - 4 * h;
+        const int qs = (cy >> 16) & 0xFF;
+        const bool rb = my_tile_row >= qs;
+        const uint32_t lo_ok = (bits >> (rb ? 2 : 0)) & 1;
+        const uint32_t hi_ok = (bits >> (rb ? 3 : 1)) & 1;
+        // keys 8q + j (j < 4) below kb: per q, clamp(kb - 8q, 0, 4) of them, all at the low bits
+        int n_lo = 0;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const int c = kb - 8 * q;
+          n_lo += c < 0 ? 0 : (c > 4 ? 4 : c);
+        }
+        const uint32_t lo_mask = n_lo >= 32 ? 0xFFFFFFFFu : ((1u << n_lo) - 1u);
+        keep = (lo_ok ? lo_mask : 0u) | (hi_ok ? ~lo_mask : 0u);
+      } else {
+        const bool extra = (cx >> 31) != 0;
+        const int64_t k0 = (int64_t)(cx & 0x7fffffffu) * kBN;
+        const int64_t nsrc = extra ? p.n_x : p.n_k;
+        const int64_t qtok = p.q_tok0 + (my_row < nrows ? my_row : (int64_t)nrows - 1);
+        const int qf_row = (int)(qtok / p.R) - p.q_frame0;
+        const uint32_t* relrow = p.rel + (int64_t)qf_row * p.words;
+        keep = 0;
+        for (int r = 0; r < 32; ++r) {
+          const int64_t key = k0 + 8 * (r >> 2) + 4 * h + (r & 3);
+          if (key < nsrc) {
+            const int64_t kf = (p.k_tok0 + key) / p.C;
+            if ((kf >> 5) < p.words && ((relrow[kf >> 5] >> (kf & 31)) & 1u)) keep |= 1u << r;
+          }
+        }
+      }
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int kk0 = 8 * (r >> 2) + (r & 3);
-        const bool k0ok = (kk0 < kb) ? lo_ok : hi_ok;
-        const bool k1ok = (kk0 + 32 < kb) ? lo_ok : hi_ok;
-        s0[r] = k0ok ? s0[r] : -INFINITY;
-        s1[r] = k1ok ? s1[r] : -INFINITY;
-      }
-    } else if (kind == kKindGeneric) {
-      const bool extra = (ent.x >> 31) != 0;
-      const int64_t k0 = (int64_t)(ent.x & 0x7fffffffu) * kBN;
-      const int64_t nsrc = extra ? p.n_x : p.n_k;
-      const int64_t qtok = p.q_tok0 + (my_row < nrows ? my_row : (int64_t)nrows - 1);
-      const int qf_row = (int)(qtok / p.R) - p.q_frame0;
-      const uint32_t* relrow = p.rel + (int64_t)qf_row * p.words;
-#pragma unroll
-      for (int r = 0; r < 32; ++r) {
-        const int kk = 32 * (r >> 4) + 8 * ((r & 15) >> 2) + 4 * h + (r & 3);
-        const int64_t key = k0 + kk;
-        bool ok = key < nsrc;
-        if (ok) {
-          const int64_t kf = (p.k_tok0 + key) / p.C;
-          ok = (kf >> 5) < p.words && ((relrow[kf >> 5] >> (kf & 31)) & 1u);
-        }
-        if (r < 16) s0[r] = ok ? s0[r] : -INFINITY;
-        else s1[r - 16] = ok ? s1[r - 16] : -INFINITY;
+        s0[r] = ((keep >> r) & 1u) ? s0[r] : -INFINITY;
+        s1[r] = ((keep >> (r + 16)) & 1u) ? s1[r] : -INFINITY;
       }
     }
 
@@ -431,6 +478,10 @@ extern "C" int lvsa_attn_fwd(const lvsa_attn_args* a, hipStream_t stream) {
   if (a->n_k) ok = ok && aligned16(a->k, a->k_str, 3) && aligned16(a->v, a->v_str, 3);
   if (a->n_x) ok = ok && aligned16(a->kx, a->kx_str, 3) && aligned16(a->vx, a->vx_str, 3);
   LVSA_REQUIRE(ok, LVSA_ERR_UNSUPPORTED, "lvsa_attn_fwd: tensors must be 16-byte aligned with 16-byte row strides");
+  // per-lane DMA offsets within a 64-row key block are 32-bit
+  auto fits = [&](int64_t row_elems) { return row_elems >= 0 && row_elems * 2 * (kBN - 1) + 2LL * a->D <= 0xFFFFFFFFLL; };
+  LVSA_REQUIRE(fits(a->k_str[1]) && fits(a->v_str[1]) && (a->n_x == 0 || (fits(a->kx_str[1]) && fits(a->vx_str[1]))),
+               LVSA_ERR_UNSUPPORTED, "lvsa_attn_fwd: key/value row stride too large");
   const int64_t work = (int64_t)a->n_tiles * a->H * a->B;
   LVSA_REQUIRE(work < (int64_t)INT32_MAX, LVSA_ERR_INVALID_ARG, "lvsa_attn_fwd: too much work");
   if (work == 0) return LVSA_OK;
