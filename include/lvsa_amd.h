@@ -147,7 +147,10 @@ LVSA_API int lvsa_plan_sizes_query(const lvsa_plan_params* p, int32_t max_row_fr
  *     word0 = (source << 31) | key-block index
  *     word1 = mask descriptor: bits 0-1 kind (0 none, 1 two-part, 2 generic),
  *             bits 2-5 allow bits (qa.lo, qa.hi, qb.lo, qb.hi),
- *             bits 8-15 key split within the block, bits 16-23 row split.     */
+ *             bits 8-15 key split within the block, bits 16-23 row split
+ *             (255 when the tile has a single query part).
+ *   block_q <= 256, block_k <= 255; lvsa_attn_fwd runs tiles of 128 or 256
+ *   query rows (lvsa_attn_args.block_q) over key blocks of 64.               */
 LVSA_API int lvsa_plan_build(const lvsa_plan_params* p, int32_t* tile_indptr, uint32_t* entries,
                     int64_t max_entries, void* workspace, int64_t workspace_bytes,
                     hipStream_t stream);
@@ -176,7 +179,8 @@ typedef struct lvsa_attn_args {
   int32_t n_q, n_k, n_x, n_tq;
   float scale;              /* softmax scale (reference: 1/sqrt(D))             */
   int32_t dtype;            /* lvsa_dtype                                       */
-  /* plan */
+  /* plan (built with block_q = 128 or 256 query rows and block_k = 64) */
+  int32_t block_q;
   const int32_t* tile_indptr;
   const uint32_t* entries;
   int32_t n_tiles, n_video_tiles;

@@ -90,6 +90,7 @@ class AttnArgs(C.Structure):
         ("B", C.c_int32), ("H", C.c_int32), ("Hkv", C.c_int32), ("D", C.c_int32),
         ("n_q", C.c_int32), ("n_k", C.c_int32), ("n_x", C.c_int32), ("n_tq", C.c_int32),
         ("scale", C.c_float), ("dtype", C.c_int32),
+        ("block_q", C.c_int32),
         ("tile_indptr", C.c_void_p), ("entries", C.c_void_p),
         ("n_tiles", C.c_int32), ("n_video_tiles", C.c_int32),
         ("rel", C.c_void_p), ("words", C.c_int32), ("R", C.c_int32), ("C", C.c_int32),

@@ -33,6 +33,9 @@ HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",
     # Keep hipcc from forming packed fp32 ops (v_pk_fma_f32 & co.).
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in arch VGPRs (the softmax reads them with VALU); AGPRs are
+    # then left to the register allocator for spills of long-lived values.
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     "-fvisibility=hidden",
     "-Wall",
 ]

@@ -22,6 +22,8 @@
 // [B, S, H, D] tensors: no gather, no transpose, no padding copies.
 #include "lvsa_common.h"
 
+#include <type_traits>
+
 namespace lvsa {
 namespace {
 
@@ -34,6 +36,7 @@ constexpr int kXcds = 8;
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef short shortx4 __attribute__((ext_vector_type(4)));
 typedef short shortx8 __attribute__((ext_vector_type(8)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) char lds_char;
 
 struct AttnParams {
@@ -76,6 +79,12 @@ struct Ops<__bf16> {
     return __builtin_amdgcn_fdot2_f32_bf16(a, one, acc, false);
   }
   __device__ static unsigned short bits(float x) { return __builtin_bit_cast(unsigned short, (__bf16)x); }
+  __device__ static v8 scale(v8 x, float a) {
+    v8 r;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r[i] = (__bf16)((float)x[i] * a);
+    return r;
+  }
 };
 
 template <>
@@ -91,6 +100,12 @@ struct Ops<_Float16> {
     return __builtin_amdgcn_fdot2(a, one, acc, false);
   }
   __device__ static unsigned short bits(float x) { return __builtin_bit_cast(unsigned short, (_Float16)x); }
+  __device__ static v8 scale(v8 x, float a) {
+    v8 r;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r[i] = (_Float16)((float)x[i] * a);
+    return r;
+  }
 };
 
 // 16-byte-chunk swizzle of LDS row r (r & 15 is all that matters).
@@ -125,11 +140,12 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
   constexpr int RB = D * 2;               // bytes per K/V row
   constexpr int NCH = RB / 16;            // 16-byte chunks per row
   constexpr int TILE = kBN * RB;          // bytes of one K or V block
-  constexpr int STAGE = 2 * TILE;
+  constexpr int STAGE = 2 * TILE;         // K block + V block
   constexpr int NI = TILE / 1024;         // 1 KiB DMA instructions per block
   constexpr int NIW = NI / kWaves;        // per wave
   constexpr int ND = D / 16;              // MFMA k-steps of S
   constexpr int NT = D / 32;              // 32-wide d tiles of O
+  constexpr int RPI = 1024 / RB;          // block rows per DMA instruction
   static_assert(NI % kWaves == 0, "tile must split evenly over waves");
 
   __shared__ __attribute__((aligned(1024))) char smem_raw[2 * STAGE];
@@ -189,16 +205,16 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
   const uint32_t krs0 = (uint32_t)(2 * p.k_str[1]), vrs0 = (uint32_t)(2 * p.v_str[1]);
   const uint32_t krs1 = (uint32_t)(2 * p.kx_str[1]), vrs1 = (uint32_t)(2 * p.vx_str[1]);
 
-  // Per-lane DMA geometry: instruction ii of this wave covers LDS bytes
-  // [(wave*NIW + ii) KiB, +1 KiB); lane -> (row within the block, byte offset
-  // of the logical 16-byte chunk it fetches).
-  uint32_t dma_row[NIW], dma_cb[NIW];
-#pragma unroll
-  for (int ii = 0; ii < NIW; ++ii) {
-    const int pos = (wave * NIW + ii) * 64 + lane;
-    const int r = pos / NCH, pc = pos % NCH;
-    dma_row[ii] = (uint32_t)r;
-    dma_cb[ii] = (uint32_t)((pc ^ swz<D>(r)) * 16);
+  // DMA geometry: instruction ii of this wave fills LDS bytes
+  // [(wave*NIW + ii) KiB, +1 KiB), i.e. block rows RPI*(wave*NIW + ii) + lane/NCH,
+  // physical chunk lane%NCH.  Because wave*NIW is a multiple of 4 (D=128) or
+  // 2 (D=64), the swizzle of those rows is  dma_c ^ ii  with a per-lane dma_c.
+  const uint32_t dma_lr = (uint32_t)(lane / NCH);
+  uint32_t dma_c16;
+  if constexpr (D == 128) {
+    dma_c16 = (uint32_t)(((lane & 15) ^ ((lane >> 4) << 2)) * 16);
+  } else {
+    dma_c16 = (uint32_t)(((lane & 7) ^ ((((lane >> 4) & 1) << 2) | (((lane >> 5) & 1) << 1))) * 16);
   }
 
   // Plan entries of this tile, 64 at a time in a VGPR (lane i holds entry
@@ -206,21 +222,18 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
   // prefetched one batch ahead so a batch switch never waits on memory.
   uint32_t ec_x = 0, ec_y = 0, en_x = 0, en_y = 0;
   int eb = e0;
-  {
-    const uint2* ents = p.entries;
-    if (e0 + lane < e1) {
-      const uint2 t = ents[e0 + lane];
-      ec_x = t.x;
-      ec_y = t.y;
-    }
-    if (e0 + 64 + lane < e1) {
-      const uint2 t = ents[e0 + 64 + lane];
-      en_x = t.x;
-      en_y = t.y;
-    }
+  if (e0 + lane < e1) {
+    const uint2 t = p.entries[e0 + lane];
+    ec_x = t.x;
+    ec_y = t.y;
+  }
+  if (e0 + 64 + lane < e1) {
+    const uint2 t = p.entries[e0 + 64 + lane];
+    en_x = t.x;
+    en_y = t.y;
   }
 
-  auto issue = [&](uint32_t ex, int stage) {
+  auto issue = [&](uint32_t ex, lds_char* ks) {
     const bool extra = (ex >> 31) != 0;
     const int64_t nsrc = extra ? p.n_x : p.n_k;
     int64_t k0 = (int64_t)(ex & 0x7fffffffu) * kBN;
@@ -228,16 +241,29 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     const uint32_t krs = extra ? krs1 : krs0, vrs = extra ? vrs1 : vrs0;
     const char* kb = (extra ? kb1 : kb0) + k0 * krs;
     const char* vb = (extra ? vb1 : vb0) + k0 * vrs;
-    // rows past the end of the source re-read its last row (masked later)
-    const uint32_t lim = (uint32_t)((nsrc - 1 - k0) < (kBN - 1) ? (nsrc - 1 - k0) : (kBN - 1));
-    lds_char* ks = smem + stage * STAGE;
     lds_char* vs = ks + TILE;
+    if (k0 + kBN <= nsrc) {
+      const uint32_t lk = dma_lr * krs, lv = dma_lr * vrs;
 #pragma unroll
-    for (int ii = 0; ii < NIW; ++ii) {
-      const uint32_t r = dma_row[ii] < lim ? dma_row[ii] : lim;
-      const int off = (wave * NIW + ii) * 1024;
-      dma16(kb + (r * krs + dma_cb[ii]), ks + off);
-      dma16(vb + (r * vrs + dma_cb[ii]), vs + off);
+      for (int ii = 0; ii < NIW; ++ii) {
+        const uint32_t row0 = (uint32_t)(RPI * (wave * NIW + ii));
+        const uint32_t c16 = dma_c16 ^ (uint32_t)(16 * (ii & (D == 128 ? 3 : 1)));
+        const int off = (wave * NIW + ii) * 1024;
+        dma16(kb + row0 * krs + (lk + c16), ks + off);
+        dma16(vb + row0 * vrs + (lv + c16), vs + off);
+      }
+    } else {
+      // last block of a source: rows past its end re-read the last row (masked later)
+      const uint32_t lim = (uint32_t)(nsrc - 1 - k0);
+#pragma unroll
+      for (int ii = 0; ii < NIW; ++ii) {
+        uint32_t r = (uint32_t)(RPI * (wave * NIW + ii)) + dma_lr;
+        r = r < lim ? r : lim;
+        const uint32_t c16 = dma_c16 ^ (uint32_t)(16 * (ii & (D == 128 ? 3 : 1)));
+        const int off = (wave * NIW + ii) * 1024;
+        dma16(kb + (r * krs + c16), ks + off);
+        dma16(vb + (r * vrs + c16), vs + off);
+      }
     }
   };
 
@@ -251,7 +277,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     for (int c = 0; c < ND; ++c) qf[c] = *reinterpret_cast<const v8*>(qp + 32 * c);
   }
 
-  // LDS read offsets.
+  // LDS read offsets (relative to a stage).
   const int sw_k = swz<D>(i32 & 15);
   int koff[ND];
 #pragma unroll
@@ -272,22 +298,19 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
   floatx16 oacc[NT];
 #pragma unroll
   for (int dt = 0; dt < NT; ++dt) oacc[dt] = floatx16{0};
-  float m_run = -1e30f;    // running max of s*scale*log2(e)
-  float l_run = 0.f;       // this lane's share of the row sum
+  float m_run = -1e30f;                  // running max of s*scale*log2(e)
+  float l4[4] = {0.f, 0.f, 0.f, 0.f};    // this lane's share of the row sum, 4 partials
   const float cs = p.scale_log2;
   const int my_tile_row = 32 * wave + i32;
 
+  // One block.  STG (0/1) is the LDS stage of this block, a compile-time
+  // constant so every LDS address is a register plus an immediate.
   uint32_t nx = 0, ny = 0;   // entry of the next block (uniform)
-  if (e0 < e1) {
-    nx = __builtin_amdgcn_readlane(ec_x, 0);
-    ny = __builtin_amdgcn_readlane(ec_y, 0);
-    issue(nx, 0);
-  }
-  for (int e = e0; e < e1; ++e) {
-    const int stage = (e - e0) & 1;
+  auto body = [&](auto stg_c, int e) {
+    constexpr int STG = decltype(stg_c)::value;
     const uint32_t cx = nx, cy = ny;
-    wait_vm0();
-    __syncthreads();
+    wait_vm0();          // this block has landed (the only DMA in flight)
+    __syncthreads();     // ... for every wave; the other stage is free again
     if (e + 1 < e1) {
       if (e + 1 - eb == 64) {
         eb += 64;
@@ -302,9 +325,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
       }
       nx = __builtin_amdgcn_readlane(ec_x, e + 1 - eb);
       ny = __builtin_amdgcn_readlane(ec_y, e + 1 - eb);
-      issue(nx, stage ^ 1);
+      issue(nx, smem + (1 - STG) * STAGE);
     }
-    const lds_char* ks = smem + stage * STAGE;
+    const lds_char* ks = smem + STG * STAGE;
     const lds_char* vs = ks + TILE;
 
     // S^T for keys [0, 32) and [32, 64) of the block.
@@ -317,7 +340,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
       s1 = O::mfma(a1, qf[c], s1);
     }
 
-    // Masks.  Bit r of `keep` covers register r%16 of sub-tile r/16, which
+    // Masks.  Bit r of `keep` covers register r%16 of key half r/16, which
     // holds key 8q + j + 4h of the block with q = r/4, j = r%4.
     const uint32_t kind = cy & 3u;
     if (kind != kKindNone) {
@@ -329,7 +352,6 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
         const bool rb = my_tile_row >= qs;
         const uint32_t lo_ok = (bits >> (rb ? 2 : 0)) & 1;
         const uint32_t hi_ok = (bits >> (rb ? 3 : 1)) & 1;
-        // keys 8q + j (j < 4) below kb: per q, clamp(kb - 8q, 0, 4) of them, all at the low bits
         int n_lo = 0;
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
@@ -361,17 +383,19 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
       }
     }
 
-    // Block row max (both halves), lazy rescale.
-    float mx = fmaxf(fmaxf(s0[0], s0[1]), s1[0]);
+    // Block row max as a tree (both key halves, then the partner lane).
+    float t8m[8];
 #pragma unroll
-    for (int r = 2; r < 16; ++r) mx = fmaxf(fmaxf(mx, s0[r]), s1[r]);
-    mx = fmaxf(mx, s1[1]);
+    for (int i = 0; i < 8; ++i) t8m[i] = fmaxf(fmaxf(s0[2 * i], s0[2 * i + 1]), fmaxf(s1[2 * i], s1[2 * i + 1]));
+    float mx = fmaxf(fmaxf(fmaxf(t8m[0], t8m[1]), fmaxf(t8m[2], t8m[3])),
+                     fmaxf(fmaxf(t8m[4], t8m[5]), fmaxf(t8m[6], t8m[7])));
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     const float mxs = mx * cs;
     if (__builtin_amdgcn_ballot_w64(mxs > m_run + 8.0f)) {
       const float m_new = fmaxf(m_run, mxs);
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-      l_run *= alpha;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) l4[i] *= alpha;
 #pragma unroll
       for (int dt = 0; dt < NT; ++dt)
 #pragma unroll
@@ -382,36 +406,47 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     // P = 2^(s*cs - m), packed to the MFMA B operand of each 16-key step.
     v8 pb[4];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const floatx16& src = (s < 2) ? s0 : s1;
-      const int base = 8 * (s & 1);
+    for (int st = 0; st < 4; ++st) {
+      const floatx16& src = (st < 2) ? s0 : s1;
+      const int base = 8 * (st & 1);
       v2 pk[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const float a = __builtin_amdgcn_exp2f(__builtin_fmaf(src[base + 2 * j], cs, -m_run));
         const float b = __builtin_amdgcn_exp2f(__builtin_fmaf(src[base + 2 * j + 1], cs, -m_run));
         pk[j] = O::pack(a, b);
-        l_run = O::dot2(pk[j], l_run);
+        l4[j] = O::dot2(pk[j], l4[j]);
       }
-      pb[s] = v8{pk[0][0], pk[0][1], pk[1][0], pk[1][1], pk[2][0], pk[2][1], pk[3][0], pk[3][1]};
+      pb[st] = v8{pk[0][0], pk[0][1], pk[1][0], pk[1][1], pk[2][0], pk[2][1], pk[3][0], pk[3][1]};
     }
 
     // O^T += V^T P^T.
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
+    for (int st = 0; st < 4; ++st) {
 #pragma unroll
       for (int dt = 0; dt < NT; ++dt) {
         const shortx4 ta = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) shortx4*)(vs + voffA[dt] + 16 * s * RB));
+            (__attribute__((address_space(3))) shortx4*)(vs + voffA[dt] + 16 * st * RB));
         const shortx4 tb = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) shortx4*)(vs + voffB[dt] + 16 * s * RB));
+            (__attribute__((address_space(3))) shortx4*)(vs + voffB[dt] + 16 * st * RB));
         const shortx8 t8 = shortx8{ta[0], ta[1], ta[2], ta[3], tb[0], tb[1], tb[2], tb[3]};
-        oacc[dt] = O::mfma(__builtin_bit_cast(v8, t8), pb[s], oacc[dt]);
+        oacc[dt] = O::mfma(__builtin_bit_cast(v8, t8), pb[st], oacc[dt]);
       }
     }
+  };
+
+  if (e0 < e1) {
+    nx = __builtin_amdgcn_readlane(ec_x, 0);
+    ny = __builtin_amdgcn_readlane(ec_y, 0);
+    issue(nx, smem);
+  }
+  for (int e = e0; e < e1; e += 2) {
+    body(std::integral_constant<int, 0>{}, e);
+    if (e + 1 < e1) body(std::integral_constant<int, 1>{}, e + 1);
   }
 
   // Epilogue: combine the row sum of both halves, normalise, store.
+  const float l_run = (l4[0] + l4[1]) + (l4[2] + l4[3]);
   const float l_tot = l_run + __shfl_xor(l_run, 32);
   if (my_row < nrows) {
     const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
@@ -433,9 +468,359 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
   }
 }
 
+// ───────────────────── v2: 64 query rows per wave, pipelined ─────────────────
+//
+// Each wave owns two 32-row sub-tiles (A, B) that share every K and V
+// fragment read from LDS (half the LDS bytes per MFMA of v1).  Blocks flow
+// through a 3-stage LDS ring; iteration j computes softmax(j) while the
+// S^T MFMAs of block j+1 are in flight, then O += P(j) V(j).  One wave per
+// SIMD (up to 512 VGPRs including AGPRs); the overlap of VALU, LDS and MFMA
+// comes from instruction-level parallelism inside the wave.
+
+constexpr int kBM2 = 256;
+constexpr int kStages2 = 3;
+
 template <int D, typename E>
-int launch(const AttnParams& prm, hipStream_t stream) {
-  hipLaunchKernelGGL((attn_fwd_kernel<D, E>), dim3(prm.total_work), dim3(kThreads), 0, stream, prm);
+__global__ __launch_bounds__(kThreads, 1) void attn_fwd_v2_kernel(AttnParams p) {
+  using O = Ops<E>;
+  using v8 = typename O::v8;
+  using v2 = typename O::v2;
+  constexpr int RB = D * 2;
+  constexpr int NCH = RB / 16;
+  constexpr int TILE = kBN * RB;
+  constexpr int STAGE = 2 * TILE;
+  constexpr int NI = TILE / 1024;
+  constexpr int NIW = NI / kWaves;
+  constexpr int ND = D / 16;
+  constexpr int NT = D / 32;
+
+  __shared__ __attribute__((aligned(1024))) char smem_raw[kStages2 * STAGE];
+  lds_char* smem = (lds_char*)smem_raw;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int h = lane >> 5;
+  const int i32 = lane & 31;
+
+  int w;
+  {
+    const int b = blockIdx.x;
+    const int per = p.total_work / kXcds, rem = p.total_work % kXcds;
+    const int x = b % kXcds, idx = b / kXcds;
+    w = x * per + (x < rem ? x : rem) + idx;
+  }
+  const int tslot = w % p.n_tiles;
+  const int rest = w / p.n_tiles;
+  const int head = rest % p.H;
+  const int batch = rest / p.H;
+  const int tile = tslot < p.n_tt ? p.n_vt + tslot : tslot - p.n_tt;
+  const bool text = tile >= p.n_vt;
+  const int hk = head / p.group;
+
+  const char* qbase;
+  char* obase;
+  int64_t qrs, ors;
+  int nrows;
+  int64_t r0;
+  float* lse;
+  if (!text) {
+    qbase = p.q + 2 * (batch * p.q_str[0] + head * p.q_str[2]);
+    obase = p.o + 2 * (batch * p.o_str[0] + head * p.o_str[2]);
+    qrs = 2 * p.q_str[1];
+    ors = 2 * p.o_str[1];
+    nrows = p.n_q;
+    r0 = (int64_t)tile * kBM2;
+    lse = p.lse ? p.lse + ((int64_t)batch * p.H + head) * p.n_q : nullptr;
+  } else {
+    qbase = p.qt + 2 * (batch * p.qt_str[0] + head * p.qt_str[2]);
+    obase = p.ot + 2 * (batch * p.ot_str[0] + head * p.ot_str[2]);
+    qrs = 2 * p.qt_str[1];
+    ors = 2 * p.ot_str[1];
+    nrows = p.n_tq;
+    r0 = (int64_t)(tile - p.n_vt) * kBM2;
+    lse = p.lse_t ? p.lse_t + ((int64_t)batch * p.H + head) * p.n_tq : nullptr;
+  }
+  const int e0 = p.tile_indptr[tile], e1 = p.tile_indptr[tile + 1];
+
+  const char* kb0 = p.k + 2 * (batch * p.k_str[0] + hk * p.k_str[2]);
+  const char* vb0 = p.v + 2 * (batch * p.v_str[0] + hk * p.v_str[2]);
+  const char* kb1 = p.n_x ? p.kx + 2 * (batch * p.kx_str[0] + hk * p.kx_str[2]) : kb0;
+  const char* vb1 = p.n_x ? p.vx + 2 * (batch * p.vx_str[0] + hk * p.vx_str[2]) : vb0;
+  const uint32_t krs0 = (uint32_t)(2 * p.k_str[1]), vrs0 = (uint32_t)(2 * p.v_str[1]);
+  const uint32_t krs1 = (uint32_t)(2 * p.kx_str[1]), vrs1 = (uint32_t)(2 * p.vx_str[1]);
+
+  uint32_t dma_row[NIW], dma_cb[NIW];
+#pragma unroll
+  for (int ii = 0; ii < NIW; ++ii) {
+    const int pos = (wave * NIW + ii) * 64 + lane;
+    const int r = pos / NCH, pc = pos % NCH;
+    dma_row[ii] = (uint32_t)r;
+    dma_cb[ii] = (uint32_t)((pc ^ swz<D>(r)) * 16);
+  }
+
+  // Plan-entry batch cache (see v1).
+  uint32_t ec_x = 0, ec_y = 0, en_x = 0, en_y = 0;
+  int eb = e0;
+  if (e0 + lane < e1) {
+    const uint2 t = p.entries[e0 + lane];
+    ec_x = t.x;
+    ec_y = t.y;
+  }
+  if (e0 + 64 + lane < e1) {
+    const uint2 t = p.entries[e0 + 64 + lane];
+    en_x = t.x;
+    en_y = t.y;
+  }
+  // Uniform entry e; advances the cache when e leaves the current batch.
+  auto entry = [&](int e, uint32_t& x, uint32_t& y) {
+    if (e - eb == 64) {
+      eb += 64;
+      ec_x = en_x;
+      ec_y = en_y;
+      en_x = en_y = 0;
+      if (eb + 64 + lane < e1) {
+        const uint2 t = p.entries[eb + 64 + lane];
+        en_x = t.x;
+        en_y = t.y;
+      }
+    }
+    x = __builtin_amdgcn_readlane(ec_x, e - eb);
+    y = __builtin_amdgcn_readlane(ec_y, e - eb);
+  };
+
+  auto issue = [&](uint32_t ex, int stage) {
+    const bool extra = (ex >> 31) != 0;
+    const int64_t nsrc = extra ? p.n_x : p.n_k;
+    int64_t k0 = (int64_t)(ex & 0x7fffffffu) * kBN;
+    if (k0 >= nsrc) k0 = 0;
+    const uint32_t krs = extra ? krs1 : krs0, vrs = extra ? vrs1 : vrs0;
+    const char* kb = (extra ? kb1 : kb0) + k0 * krs;
+    const char* vb = (extra ? vb1 : vb0) + k0 * vrs;
+    const uint32_t lim = (uint32_t)((nsrc - 1 - k0) < (kBN - 1) ? (nsrc - 1 - k0) : (kBN - 1));
+    lds_char* ks = smem + stage * STAGE;
+    lds_char* vs = ks + TILE;
+#pragma unroll
+    for (int ii = 0; ii < NIW; ++ii) {
+      const uint32_t r = dma_row[ii] < lim ? dma_row[ii] : lim;
+      const int off = (wave * NIW + ii) * 1024;
+      dma16(kb + (r * krs + dma_cb[ii]), ks + off);
+      dma16(vb + (r * vrs + dma_cb[ii]), vs + off);
+    }
+  };
+
+  // Q fragments of both sub-tiles.
+  v8 qa[ND], qb[ND];
+  const int64_t row_a = r0 + 64 * wave + i32, row_b = row_a + 32;
+  {
+    const int64_t ra = row_a < nrows ? row_a : (int64_t)nrows - 1;
+    const int64_t rb = row_b < nrows ? row_b : (int64_t)nrows - 1;
+    const char* pa = qbase + ra * qrs + 16 * h;
+    const char* pb = qbase + rb * qrs + 16 * h;
+#pragma unroll
+    for (int c = 0; c < ND; ++c) {
+      qa[c] = *reinterpret_cast<const v8*>(pa + 32 * c);
+      qb[c] = *reinterpret_cast<const v8*>(pb + 32 * c);
+    }
+  }
+
+  const int sw_k = swz<D>(i32 & 15);
+  int koff[ND];
+#pragma unroll
+  for (int c = 0; c < ND; ++c) koff[c] = i32 * RB + ((((2 * c + h) ^ sw_k)) << 4);
+  const int g16 = lane & 15;
+  const int rowA = 4 * h + (g16 >> 2);
+  const int sw_a = swz<D>(rowA), sw_b = swz<D>(rowA + 8);
+  const int dgrp = (lane >> 4) & 1;
+  int voffA[NT], voffB[NT];
+#pragma unroll
+  for (int dt = 0; dt < NT; ++dt) {
+    const int chunk = 4 * dt + 2 * dgrp + ((lane & 3) >> 1);
+    const int inb = (lane & 1) * 8;
+    voffA[dt] = rowA * RB + ((chunk ^ sw_a) << 4) + inb;
+    voffB[dt] = (rowA + 8) * RB + ((chunk ^ sw_b) << 4) + inb;
+  }
+
+  floatx16 oa[NT], ob[NT];
+#pragma unroll
+  for (int dt = 0; dt < NT; ++dt) {
+    oa[dt] = floatx16{0};
+    ob[dt] = floatx16{0};
+  }
+  float m_a = -1e30f, m_b = -1e30f, l_a = 0.f, l_b = 0.f;
+  const float cs = p.scale_log2;
+  const int trow_a = 64 * wave + i32, trow_b = trow_a + 32;
+
+  // S^T of one block for both sub-tiles (K fragments shared).
+  auto qk = [&](const lds_char* ks, floatx16* sa, floatx16* sb) {
+    sa[0] = sa[1] = sb[0] = sb[1] = floatx16{0};
+#pragma unroll
+    for (int c = 0; c < ND; ++c) {
+      const v8 k0f = *reinterpret_cast<const __attribute__((address_space(3))) v8*>(ks + koff[c]);
+      const v8 k1f = *reinterpret_cast<const __attribute__((address_space(3))) v8*>(ks + koff[c] + 32 * RB);
+      sa[0] = O::mfma(k0f, qa[c], sa[0]);
+      sb[0] = O::mfma(k0f, qb[c], sb[0]);
+      sa[1] = O::mfma(k1f, qa[c], sa[1]);
+      sb[1] = O::mfma(k1f, qb[c], sb[1]);
+    }
+  };
+
+  // Mask keep-bits of one sub-tile (bit r: register r%16 of key half r/16).
+  auto keep_bits = [&](uint32_t cx, uint32_t cy, int trow, int64_t row) -> uint32_t {
+    const uint32_t kind = cy & 3u;
+    if (kind == kKindTwoPart) {
+      const int bits = (cy >> 2) & 0xF;
+      const int kb = (int)((cy >> 8) & 0xFF) - 4 * h;
+      const int qs = (cy >> 16) & 0xFF;
+      const bool rb = trow >= qs;
+      const uint32_t lo_ok = (bits >> (rb ? 2 : 0)) & 1;
+      const uint32_t hi_ok = (bits >> (rb ? 3 : 1)) & 1;
+      int n_lo = 0;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int c = kb - 8 * q;
+        n_lo += c < 0 ? 0 : (c > 4 ? 4 : c);
+      }
+      const uint32_t lo_mask = n_lo >= 32 ? 0xFFFFFFFFu : ((1u << n_lo) - 1u);
+      return (lo_ok ? lo_mask : 0u) | (hi_ok ? ~lo_mask : 0u);
+    }
+    const bool extra = (cx >> 31) != 0;
+    const int64_t k0 = (int64_t)(cx & 0x7fffffffu) * kBN;
+    const int64_t nsrc = extra ? p.n_x : p.n_k;
+    const int64_t qtok = p.q_tok0 + (row < nrows ? row : (int64_t)nrows - 1);
+    const int qf_row = (int)(qtok / p.R) - p.q_frame0;
+    const uint32_t* relrow = p.rel + (int64_t)qf_row * p.words;
+    uint32_t keep = 0;
+    for (int r = 0; r < 32; ++r) {
+      const int64_t key = k0 + 8 * (r >> 2) + 4 * h + (r & 3);
+      if (key < nsrc) {
+        const int64_t kf = (p.k_tok0 + key) / p.C;
+        if ((kf >> 5) < p.words && ((relrow[kf >> 5] >> (kf & 31)) & 1u)) keep |= 1u << r;
+      }
+    }
+    return keep;
+  };
+
+  // Online softmax of one sub-tile: S (2 x 16 regs) -> packed P (4 x v8).
+  auto softmax = [&](floatx16* s, uint32_t cx, uint32_t cy, int trow, int64_t row, float& m_run, float& l_run,
+                     floatx16* oacc, v8* pk8) {
+    if ((cy & 3u) != kKindNone) {
+      const uint32_t keep = keep_bits(cx, cy, trow, row);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        s[0][r] = ((keep >> r) & 1u) ? s[0][r] : -INFINITY;
+        s[1][r] = ((keep >> (r + 16)) & 1u) ? s[1][r] : -INFINITY;
+      }
+    }
+    float mx = fmaxf(fmaxf(s[0][0], s[0][1]), s[1][0]);
+#pragma unroll
+    for (int r = 2; r < 16; ++r) mx = fmaxf(fmaxf(mx, s[0][r]), s[1][r]);
+    mx = fmaxf(mx, s[1][1]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float mxs = mx * cs;
+    if (__builtin_amdgcn_ballot_w64(mxs > m_run + 8.0f)) {
+      const float m_new = fmaxf(m_run, mxs);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < NT; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
+      m_run = m_new;
+    }
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      const floatx16& src = s[st >> 1];
+      const int base = 8 * (st & 1);
+      v2 pk[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float a = __builtin_amdgcn_exp2f(__builtin_fmaf(src[base + 2 * j], cs, -m_run));
+        const float b = __builtin_amdgcn_exp2f(__builtin_fmaf(src[base + 2 * j + 1], cs, -m_run));
+        pk[j] = O::pack(a, b);
+        l_run = O::dot2(pk[j], l_run);
+      }
+      pk8[st] = v8{pk[0][0], pk[0][1], pk[1][0], pk[1][1], pk[2][0], pk[2][1], pk[3][0], pk[3][1]};
+    }
+  };
+
+  // O^T += V^T P^T for both sub-tiles (V fragments shared).
+  auto pv = [&](const lds_char* vs, const v8* pa8, const v8* pb8) {
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+#pragma unroll
+      for (int dt = 0; dt < NT; ++dt) {
+        const shortx4 ta = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) shortx4*)(vs + voffA[dt] + 16 * st * RB));
+        const shortx4 tb = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) shortx4*)(vs + voffB[dt] + 16 * st * RB));
+        const v8 vf = __builtin_bit_cast(v8, shortx8{ta[0], ta[1], ta[2], ta[3], tb[0], tb[1], tb[2], tb[3]});
+        oa[dt] = O::mfma(vf, pa8[st], oa[dt]);
+        ob[dt] = O::mfma(vf, pb8[st], ob[dt]);
+      }
+    }
+  };
+
+  // Pipeline over the n blocks of the tile (stage of block j = j % 3):
+  //   iteration j:  S = K(j) Q^T;  O += P(j-1) V(j-1);  P(j) = softmax(S)
+  // so the softmax VALU of block j runs while the P V MFMAs of block j-1 are
+  // in the matrix pipe.  The DMA of block j+1 is issued at the top of
+  // iteration j, after the barrier that retires block j-2's stage.
+  const int n = e1 - e0;
+  floatx16 sa[2], sb[2];
+  v8 pa8[4], pb8[4];
+  uint32_t cx = 0, cy = 0;      // entry of block j
+  uint32_t nx = 0, ny = 0;      // entry of block j+1
+  if (n > 0) {
+    entry(e0, cx, cy);
+    issue(cx, 0);
+    if (n > 1) entry(e0 + 1, nx, ny);
+  }
+  for (int j = 0; j < n; ++j) {
+    const int stage = j % kStages2;
+    wait_vm0();          // block j has landed (the only DMA in flight)
+    __syncthreads();     // ... for every wave; block j-2's stage is retired
+    if (j + 1 < n) issue(nx, (j + 1) % kStages2);
+    qk(smem + stage * STAGE, sa, sb);
+    if (j > 0) pv(smem + ((j + kStages2 - 1) % kStages2) * STAGE + TILE, pa8, pb8);
+    softmax(sa, cx, cy, trow_a, row_a, m_a, l_a, oa, pa8);
+    softmax(sb, cx, cy, trow_b, row_b, m_b, l_b, ob, pb8);
+    cx = nx;
+    cy = ny;
+    if (j + 2 < n) entry(e0 + j + 2, nx, ny);
+  }
+  if (n > 0) pv(smem + ((n - 1) % kStages2) * STAGE + TILE, pa8, pb8);
+
+  // Epilogue for both sub-tiles.
+  auto store = [&](floatx16* oacc, float l_run, float m_run, int64_t row) {
+    const float l_tot = l_run + __shfl_xor(l_run, 32);
+    if (row < nrows) {
+      const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+      char* op = obase + row * ors;
+#pragma unroll
+      for (int dt = 0; dt < NT; ++dt) {
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq) {
+          const int d0 = 32 * dt + 8 * rq + 4 * h;
+          uint2 pk;
+          pk.x = (uint32_t)O::bits(oacc[dt][4 * rq] * inv) | ((uint32_t)O::bits(oacc[dt][4 * rq + 1] * inv) << 16);
+          pk.y = (uint32_t)O::bits(oacc[dt][4 * rq + 2] * inv) | ((uint32_t)O::bits(oacc[dt][4 * rq + 3] * inv) << 16);
+          *reinterpret_cast<uint2*>(op + 2 * d0) = pk;
+        }
+      }
+      if (lse && h == 0) lse[row] = l_tot > 0.f ? (m_run + __log2f(l_tot)) * 0.69314718055994530942f : -INFINITY;
+    }
+  };
+  store(oa, l_a, m_a, row_a);
+  store(ob, l_b, m_b, row_b);
+}
+
+template <int D, typename E>
+int launch(const AttnParams& prm, int block_q, hipStream_t stream) {
+  if (block_q == kBM2) {
+    hipLaunchKernelGGL((attn_fwd_v2_kernel<D, E>), dim3(prm.total_work), dim3(kThreads), 0, stream, prm);
+  } else {
+    hipLaunchKernelGGL((attn_fwd_kernel<D, E>), dim3(prm.total_work), dim3(kThreads), 0, stream, prm);
+  }
   return launch_status("lvsa_attn_fwd");
 }
 
@@ -463,10 +848,12 @@ extern "C" int lvsa_attn_fwd(const lvsa_attn_args* a, hipStream_t stream) {
   LVSA_REQUIRE(a->n_q >= 0 && a->n_k >= 0 && a->n_x >= 0 && a->n_tq >= 0, LVSA_ERR_INVALID_ARG,
                "lvsa_attn_fwd: negative length");
   LVSA_REQUIRE(a->tile_indptr && a->entries, LVSA_ERR_INVALID_ARG, "lvsa_attn_fwd: missing plan");
-  const int n_vt = (int)ceil_div(a->n_q, kBM), n_tt = (int)ceil_div(a->n_tq, kBM);
+  LVSA_REQUIRE(a->block_q == kBM || a->block_q == kBM2, LVSA_ERR_UNSUPPORTED,
+               "lvsa_attn_fwd: block_q %d (the kernels tile 128 or 256 query rows)", a->block_q);
+  const int n_vt = (int)ceil_div(a->n_q, a->block_q), n_tt = (int)ceil_div(a->n_tq, a->block_q);
   LVSA_REQUIRE(a->n_video_tiles == n_vt && a->n_tiles == n_vt + n_tt, LVSA_ERR_INVALID_ARG,
-               "lvsa_attn_fwd: plan has %d/%d tiles, expected %d/%d (block_q must be %d)", a->n_video_tiles,
-               a->n_tiles, n_vt, n_vt + n_tt, kBM);
+               "lvsa_attn_fwd: plan has %d/%d tiles, expected %d/%d for block_q %d", a->n_video_tiles,
+               a->n_tiles, n_vt, n_vt + n_tt, a->block_q);
   LVSA_REQUIRE(a->n_q == 0 || (a->q && a->o), LVSA_ERR_INVALID_ARG, "lvsa_attn_fwd: null q/o");
   LVSA_REQUIRE(a->n_tq == 0 || (a->qt && a->ot), LVSA_ERR_INVALID_ARG, "lvsa_attn_fwd: null text q/o");
   LVSA_REQUIRE(a->n_k == 0 || (a->k && a->v), LVSA_ERR_INVALID_ARG, "lvsa_attn_fwd: null k/v");
@@ -529,6 +916,8 @@ extern "C" int lvsa_attn_fwd(const lvsa_attn_args* a, hipStream_t stream) {
   p.q_tok0 = a->q_tok0;
   p.k_tok0 = a->k_tok0;
   p.total_work = (int)work;
-  if (a->D == 128) return a->dtype == LVSA_BF16 ? launch<128, __bf16>(p, stream) : launch<128, _Float16>(p, stream);
-  return a->dtype == LVSA_BF16 ? launch<64, __bf16>(p, stream) : launch<64, _Float16>(p, stream);
+  const int bq = a->block_q;
+  if (a->D == 128)
+    return a->dtype == LVSA_BF16 ? launch<128, __bf16>(p, bq, stream) : launch<128, _Float16>(p, bq, stream);
+  return a->dtype == LVSA_BF16 ? launch<64, __bf16>(p, bq, stream) : launch<64, _Float16>(p, bq, stream);
 }

@@ -9,6 +9,7 @@ from __future__ import annotations
 
 import ctypes as C
 import math
+import os
 from dataclasses import dataclass
 from typing import Optional, Sequence, Tuple
 
@@ -18,6 +19,11 @@ from . import _capi as capi
 
 _DTYPES = {torch.bfloat16: capi.LVSA_BF16, torch.float16: capi.LVSA_FP16}
 SUPPORTED_HEAD_DIMS = (64, 128)
+
+
+def attn_block_q() -> int:
+    """Query rows per attention tile: 256 (64 rows per wave, pipelined) or 128."""
+    return int(os.environ.get("LVSA_ATTN_BLOCK_Q", "128"))
 
 
 def _stream(device: torch.device) -> int:
@@ -134,7 +140,7 @@ class BlockPlan:
 
 def plan_build(rel: Optional[torch.Tensor], *, n_q: int, n_k: int, n_x: int = 0, n_tq: int = 0,
                R: int = 1, Cf: int = 1, q_tok0: int = 0, k_tok0: int = 0, q_frame0: int = 0,
-               max_row_frames: int = 0, block_q: int = capi.ATTN_BLOCK_Q, block_k: int = capi.ATTN_BLOCK_K,
+               max_row_frames: int = 0, block_q: Optional[int] = None, block_k: int = capi.ATTN_BLOCK_K,
                device: Optional[torch.device] = None) -> BlockPlan:
     """Refine a frame relation (bitmap rows x words, int32) to token blocks."""
     if rel is not None:
@@ -144,6 +150,8 @@ def plan_build(rel: Optional[torch.Tensor], *, n_q: int, n_k: int, n_x: int = 0,
     if device is None or torch.device(device).type != "cuda":
         raise RuntimeError("lvsa_plan_build runs on the GPU only")
     device = torch.device(device)
+    if block_q is None:
+        block_q = attn_block_q()
     p = capi.PlanParams()
     p.n_q, p.n_k, p.n_x, p.n_tq = n_q, n_k, n_x, n_tq
     p.R, p.C = R, Cf
@@ -249,6 +257,7 @@ def attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, plan: BlockPlan,
     a.n_q, a.n_k, a.n_x, a.n_tq = n_q, k.shape[1], n_x, n_tq
     a.scale = float(scale) if scale is not None else 1.0 / math.sqrt(D)
     a.dtype = _DTYPES[dtype]
+    a.block_q = plan.block_q
     a.tile_indptr, a.entries = plan.tile_indptr.data_ptr(), plan.entries.data_ptr()
     a.n_tiles, a.n_video_tiles = plan.n_tiles, plan.n_video_tiles
     a.rel = pp.rel
