@@ -133,7 +133,7 @@ def main(argv=None) -> int:
         t0 = time.perf_counter()
         m = lv.LVSAMetadata.build(total_latent_frames=T, num_patches=P, window_size=W, n_first_frames=1,
                                   key_frame_interval=kfi, rank=0, world=1, keyframe_offset=off)
-        m.full_plan(dev, N, N, n_text, n_text)
+        m.full_plan(dev, N, N, n_text, n_text, D)
         torch.cuda.synchronize()
         build_ms.append(1e3 * (time.perf_counter() - t0))
         metas[off] = m

@@ -68,7 +68,7 @@ class BlockSparseAttentionWrapper:
         n_blocks_k = N // C
         self._bitmap, status = hip_ops.csr_to_bitmap(indptr, indices, n_blocks_k)
         self._plan = hip_ops.plan_build(self._bitmap, n_q=M, n_k=N, R=R, Cf=C,
-                                        max_row_frames=max(1, n_blocks_k), device=device)
+                                        max_row_frames=max(1, n_blocks_k), head_dim=head_dim, device=device)
         self._shape = (M, N, num_qo_heads, num_kv_heads, head_dim)
         self._scale = sm_scale
         self._status = status
@@ -105,10 +105,11 @@ def single_prefill_with_kv_cache(q: torch.Tensor, k: torch.Tensor, v: torch.Tens
     if causal:
         raise NotImplementedError("causal prefill is not part of the LVSA path")
     hip_ops._require_device(q, "q")
-    key = (q.device, q.shape[0], k.shape[0])
+    key = (q.device, q.shape[0], k.shape[0], hip_ops.attn_block_q(q.shape[-1]))
     plan = _DENSE_PLANS.get(key)
     if plan is None:
-        plan = hip_ops.plan_build(None, n_q=0, n_k=k.shape[0], n_tq=q.shape[0], device=q.device)
+        plan = hip_ops.plan_build(None, n_q=0, n_k=k.shape[0], n_tq=q.shape[0], head_dim=q.shape[-1],
+                                  device=q.device)
         _DENSE_PLANS[key] = plan
     # Dense rows are the kernel's "text query" tiles: every key block, no mask.
     qt = q.unsqueeze(0)

@@ -468,40 +468,104 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
   }
 }
 
-// ───────────────────── v2: 64 query rows per wave, pipelined ─────────────────
+// ───────────── ping-pong kernel: 8 waves, 256 query rows per tile ─────────────
 //
-// Each wave owns two 32-row sub-tiles (A, B) that share every K and V
-// fragment read from LDS (half the LDS bytes per MFMA of v1).  Blocks flow
-// through a 3-stage LDS ring; iteration j computes softmax(j) while the
-// S^T MFMAs of block j+1 are in flight, then O += P(j) V(j).  One wave per
-// SIMD (up to 512 VGPRs including AGPRs); the overlap of VALU, LDS and MFMA
-// comes from instruction-level parallelism inside the wave.
+// Waves w and w + 4 of a 512-thread workgroup run on the same SIMD.  Group 0
+// (waves 0-3) and group 1 (waves 4-7) hold 32 query rows per wave and walk
+// the same key blocks one phase apart, separated by workgroup barriers:
+//
+//   phase        0       1       2       3       4   ...
+//   group 0    M(0)    S(0)    M(1)    S(1)    M(2)
+//   group 1     -      M(0)    S(0)    M(1)    S(1)
+//
+// M(j): S^T of block j and O += P V of block j - 1 (MFMA fed from LDS);
+// S(j): mask, row max, exp and row sums of block j (VALU).  At every phase
+// each SIMD runs one wave's MFMAs under the other wave's softmax.  K/V blocks
+// rotate through a 4-stage LDS ring: block b is read from phase 2b (S^T,
+// group 0) to phase 2b + 3 (P V, group 1), and group 1 DMAs block m + 2
+// during its softmax phase 2m, about three phases before its first use.
+// The four K tiles sit at [0, 4 TILE) and the four V tiles above them, and
+// the phase loop is unrolled over 8 phases so every stage is a compile-time
+// constant: each LDS read is a VGPR plus an immediate.  M phases are
+// branch-free: the V tile of stage 3 starts zeroed and P starts at 0, so the
+// P V of block -1 in M(0) adds zero, and the S^T of block n computed in M(n)
+// is never used.
 
-constexpr int kBM2 = 256;
-constexpr int kStages2 = 3;
+constexpr int kPPWaves = 8;
+constexpr int kPPThreads = 64 * kPPWaves;
+constexpr int kPPBM = 32 * kPPWaves;
+constexpr int kPPStages = 4;
+
+// Workgroup barrier that nothing crosses: the memory clobber orders LDS and
+// global accesses, the scheduling barriers keep arithmetic (the exps of a
+// softmax phase) from drifting into the next phase.
+__device__ __forceinline__ void wg_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_barrier" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// s_waitcnt vmcnt(N) with expcnt and lgkmcnt left at their maxima.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 16, "vmcnt immediate");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | N);
+}
+
+// v_permlane32_swap on a copy of x: afterwards {a, b} hold x of lanes 0-31
+// and x of lanes 32-63 (one in each), so max(a, b) / a + b combine lanes l
+// and l ^ 32.  Written as asm with both registers in/out: the two-result
+// builtin of this toolchain loses its second result.  The s_nops cover the
+// VALU-write -> permlane-read hazard and the reads of its results.
+__device__ __forceinline__ void swap_halves(float& a, float& b) {
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+// IEEE maximum (v_maximum3_f32 when chained): unlike fmaxf it needs no
+// canonicalisation of MFMA results first.
+__device__ __forceinline__ float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+__device__ __forceinline__ float max_halves(float x) {
+  float a = x, b = x;
+  swap_halves(a, b);
+  return vmax(a, b);
+}
+// Materialise x here: keeps the compiler from sinking the computation of a
+// phase's results across the barrier into the phase that consumes them.
+template <typename T>
+__device__ __forceinline__ void pin(T& x) {
+  asm volatile("" : "+v"(x));
+}
+__device__ __forceinline__ float sum_halves(float x) {
+  float a = x, b = x;
+  swap_halves(a, b);
+  return a + b;
+}
 
 template <int D, typename E>
-__global__ __launch_bounds__(kThreads, 1) void attn_fwd_v2_kernel(AttnParams p) {
+__global__ __launch_bounds__(kPPThreads, 1) void attn_fwd_pp_kernel(AttnParams p) {
   using O = Ops<E>;
   using v8 = typename O::v8;
   using v2 = typename O::v2;
-  constexpr int RB = D * 2;
-  constexpr int NCH = RB / 16;
-  constexpr int TILE = kBN * RB;
-  constexpr int STAGE = 2 * TILE;
-  constexpr int NI = TILE / 1024;
-  constexpr int NIW = NI / kWaves;
-  constexpr int ND = D / 16;
-  constexpr int NT = D / 32;
+  constexpr int RB = D * 2;               // bytes per K/V row
+  constexpr int NCH = RB / 16;            // 16-byte chunks per row
+  constexpr int TILE = kBN * RB;          // bytes of one K or V block
+  constexpr int NI = TILE / 1024;         // 1 KiB DMA instructions per block
+  constexpr int NIW = NI / 4;             // per group-1 wave
+  constexpr int ND = D / 16;              // MFMA k-steps of S
+  constexpr int NT = D / 32;              // 32-wide d tiles of O
+  constexpr int RPI = 1024 / RB;          // block rows per DMA instruction
+  static_assert(NI % 4 == 0, "tile must split evenly over the DMA waves");
 
-  __shared__ __attribute__((aligned(1024))) char smem_raw[kStages2 * STAGE];
+  __shared__ __attribute__((aligned(1024))) char smem_raw[2 * kPPStages * TILE];
   lds_char* smem = (lds_char*)smem_raw;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int grp = wave >> 2;      // 0: MFMA on even phases, 1: on odd phases
+  const int dw = wave & 3;        // DMA slot of a group-1 wave
   const int h = lane >> 5;
   const int i32 = lane & 31;
 
+  // XCD-aware work order: consecutive work items stay on one XCD (shared L2).
   int w;
   {
     const int b = blockIdx.x;
@@ -513,7 +577,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_fwd_v2_kernel(AttnParams p) 
   const int rest = w / p.n_tiles;
   const int head = rest % p.H;
   const int batch = rest / p.H;
-  const int tile = tslot < p.n_tt ? p.n_vt + tslot : tslot - p.n_tt;
+  const int tile = tslot < p.n_tt ? p.n_vt + tslot : tslot - p.n_tt;  // text tiles (longest) first
   const bool text = tile >= p.n_vt;
   const int hk = head / p.group;
 
@@ -529,7 +593,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_fwd_v2_kernel(AttnParams p) 
     qrs = 2 * p.q_str[1];
     ors = 2 * p.o_str[1];
     nrows = p.n_q;
-    r0 = (int64_t)tile * kBM2;
+    r0 = (int64_t)tile * kPPBM;
     lse = p.lse ? p.lse + ((int64_t)batch * p.H + head) * p.n_q : nullptr;
   } else {
     qbase = p.qt + 2 * (batch * p.qt_str[0] + head * p.qt_str[2]);
@@ -537,10 +601,11 @@ __global__ __launch_bounds__(kThreads, 1) void attn_fwd_v2_kernel(AttnParams p) 
     qrs = 2 * p.qt_str[1];
     ors = 2 * p.ot_str[1];
     nrows = p.n_tq;
-    r0 = (int64_t)(tile - p.n_vt) * kBM2;
+    r0 = (int64_t)(tile - p.n_vt) * kPPBM;
     lse = p.lse_t ? p.lse_t + ((int64_t)batch * p.H + head) * p.n_tq : nullptr;
   }
   const int e0 = p.tile_indptr[tile], e1 = p.tile_indptr[tile + 1];
+  const int n = e1 - e0;
 
   const char* kb0 = p.k + 2 * (batch * p.k_str[0] + hk * p.k_str[2]);
   const char* vb0 = p.v + 2 * (batch * p.v_str[0] + hk * p.v_str[2]);
@@ -549,16 +614,21 @@ __global__ __launch_bounds__(kThreads, 1) void attn_fwd_v2_kernel(AttnParams p) 
   const uint32_t krs0 = (uint32_t)(2 * p.k_str[1]), vrs0 = (uint32_t)(2 * p.v_str[1]);
   const uint32_t krs1 = (uint32_t)(2 * p.kx_str[1]), vrs1 = (uint32_t)(2 * p.vx_str[1]);
 
-  uint32_t dma_row[NIW], dma_cb[NIW];
-#pragma unroll
-  for (int ii = 0; ii < NIW; ++ii) {
-    const int pos = (wave * NIW + ii) * 64 + lane;
-    const int r = pos / NCH, pc = pos % NCH;
-    dma_row[ii] = (uint32_t)r;
-    dma_cb[ii] = (uint32_t)((pc ^ swz<D>(r)) * 16);
+  // DMA geometry of a group-1 wave: instruction ii fills LDS bytes
+  // [(dw*NIW + ii) KiB, +1 KiB) of a tile, i.e. block rows
+  // RPI*(dw*NIW + ii) + lane/NCH, physical chunk lane%NCH.  dw*NIW is a
+  // multiple of 4 (D=128) or 2 (D=64), so the swizzle of those rows is
+  // dma_c ^ ii with a per-lane dma_c.
+  const uint32_t dma_lr = (uint32_t)(lane / NCH);
+  uint32_t dma_c16;
+  if constexpr (D == 128) {
+    dma_c16 = (uint32_t)(((lane & 15) ^ ((lane >> 4) << 2)) * 16);
+  } else {
+    dma_c16 = (uint32_t)(((lane & 7) ^ ((((lane >> 4) & 1) << 2) | (((lane >> 5) & 1) << 1))) * 16);
   }
 
-  // Plan-entry batch cache (see v1).
+  // Plan entries, 64 per VGPR batch (lane i holds entry eb + i) with the
+  // following batch prefetched; a uniform entry is read with v_readlane.
   uint32_t ec_x = 0, ec_y = 0, en_x = 0, en_y = 0;
   int eb = e0;
   if (e0 + lane < e1) {
@@ -571,9 +641,20 @@ __global__ __launch_bounds__(kThreads, 1) void attn_fwd_v2_kernel(AttnParams p) 
     en_x = t.x;
     en_y = t.y;
   }
-  // Uniform entry e; advances the cache when e leaves the current batch.
-  auto entry = [&](int e, uint32_t& x, uint32_t& y) {
-    if (e - eb == 64) {
+  // entry e, eb <= e < eb + 128
+  auto entry = [&](int e, uint32_t& x, uint32_t& y) __attribute__((always_inline)) {
+    const int d = e - eb;
+    if (d < 64) {
+      x = __builtin_amdgcn_readlane(ec_x, d);
+      y = __builtin_amdgcn_readlane(ec_y, d);
+    } else {
+      x = __builtin_amdgcn_readlane(en_x, d - 64);
+      y = __builtin_amdgcn_readlane(en_y, d - 64);
+    }
+  };
+  // slide the batches once no entry below e is needed any more
+  auto advance = [&](int e) __attribute__((always_inline)) {
+    if (e - eb >= 64) {
       eb += 64;
       ec_x = en_x;
       ec_y = en_y;
@@ -584,51 +665,58 @@ __global__ __launch_bounds__(kThreads, 1) void attn_fwd_v2_kernel(AttnParams p) 
         en_y = t.y;
       }
     }
-    x = __builtin_amdgcn_readlane(ec_x, e - eb);
-    y = __builtin_amdgcn_readlane(ec_y, e - eb);
   };
 
-  auto issue = [&](uint32_t ex, int stage) {
+  auto issue = [&](uint32_t ex, lds_char* ks, lds_char* vs) __attribute__((always_inline)) {
     const bool extra = (ex >> 31) != 0;
     const int64_t nsrc = extra ? p.n_x : p.n_k;
     int64_t k0 = (int64_t)(ex & 0x7fffffffu) * kBN;
-    if (k0 >= nsrc) k0 = 0;
+    if (k0 >= nsrc) k0 = 0;  // never produced by the plan; keeps every DMA in bounds
     const uint32_t krs = extra ? krs1 : krs0, vrs = extra ? vrs1 : vrs0;
     const char* kb = (extra ? kb1 : kb0) + k0 * krs;
     const char* vb = (extra ? vb1 : vb0) + k0 * vrs;
-    const uint32_t lim = (uint32_t)((nsrc - 1 - k0) < (kBN - 1) ? (nsrc - 1 - k0) : (kBN - 1));
-    lds_char* ks = smem + stage * STAGE;
-    lds_char* vs = ks + TILE;
+    if (k0 + kBN <= nsrc) {
+      const uint32_t lk = dma_lr * krs, lv = dma_lr * vrs;
 #pragma unroll
-    for (int ii = 0; ii < NIW; ++ii) {
-      const uint32_t r = dma_row[ii] < lim ? dma_row[ii] : lim;
-      const int off = (wave * NIW + ii) * 1024;
-      dma16(kb + (r * krs + dma_cb[ii]), ks + off);
-      dma16(vb + (r * vrs + dma_cb[ii]), vs + off);
+      for (int ii = 0; ii < NIW; ++ii) {
+        const uint32_t row0 = (uint32_t)(RPI * (dw * NIW + ii));
+        const uint32_t c16 = dma_c16 ^ (uint32_t)(16 * (ii & (D == 128 ? 3 : 1)));
+        const int off = (dw * NIW + ii) * 1024;
+        dma16(kb + row0 * krs + (lk + c16), ks + off);
+        dma16(vb + row0 * vrs + (lv + c16), vs + off);
+      }
+    } else {
+      // last block of a source: rows past its end re-read the last row (masked later)
+      const uint32_t lim = (uint32_t)(nsrc - 1 - k0);
+#pragma unroll
+      for (int ii = 0; ii < NIW; ++ii) {
+        uint32_t r = (uint32_t)(RPI * (dw * NIW + ii)) + dma_lr;
+        r = r < lim ? r : lim;
+        const uint32_t c16 = dma_c16 ^ (uint32_t)(16 * (ii & (D == 128 ? 3 : 1)));
+        const int off = (dw * NIW + ii) * 1024;
+        dma16(kb + (r * krs + c16), ks + off);
+        dma16(vb + (r * vrs + c16), vs + off);
+      }
     }
   };
 
-  // Q fragments of both sub-tiles.
-  v8 qa[ND], qb[ND];
-  const int64_t row_a = r0 + 64 * wave + i32, row_b = row_a + 32;
+  // Q fragments (B operand of S^T = K Q^T): row i32 of this wave, d = 16c + 8h .. +7.
+  v8 qf[ND];
+  const int64_t my_row = r0 + 32 * wave + i32;
   {
-    const int64_t ra = row_a < nrows ? row_a : (int64_t)nrows - 1;
-    const int64_t rb = row_b < nrows ? row_b : (int64_t)nrows - 1;
-    const char* pa = qbase + ra * qrs + 16 * h;
-    const char* pb = qbase + rb * qrs + 16 * h;
+    const int64_t qr = my_row < nrows ? my_row : (int64_t)nrows - 1;
+    const char* qp = qbase + qr * qrs + 16 * h;
 #pragma unroll
-    for (int c = 0; c < ND; ++c) {
-      qa[c] = *reinterpret_cast<const v8*>(pa + 32 * c);
-      qb[c] = *reinterpret_cast<const v8*>(pb + 32 * c);
-    }
+    for (int c = 0; c < ND; ++c) qf[c] = *reinterpret_cast<const v8*>(qp + 32 * c);
   }
 
+  // LDS read offsets (relative to a stage).
   const int sw_k = swz<D>(i32 & 15);
   int koff[ND];
 #pragma unroll
   for (int c = 0; c < ND; ++c) koff[c] = i32 * RB + ((((2 * c + h) ^ sw_k)) << 4);
   const int g16 = lane & 15;
-  const int rowA = 4 * h + (g16 >> 2);
+  const int rowA = 4 * h + (g16 >> 2);            // + 16*s (+8 for the second read)
   const int sw_a = swz<D>(rowA), sw_b = swz<D>(rowA + 8);
   const int dgrp = (lane >> 4) & 1;
   int voffA[NT], voffB[NT];
@@ -636,188 +724,302 @@ __global__ __launch_bounds__(kThreads, 1) void attn_fwd_v2_kernel(AttnParams p) 
   for (int dt = 0; dt < NT; ++dt) {
     const int chunk = 4 * dt + 2 * dgrp + ((lane & 3) >> 1);
     const int inb = (lane & 1) * 8;
-    voffA[dt] = rowA * RB + ((chunk ^ sw_a) << 4) + inb;
-    voffB[dt] = (rowA + 8) * RB + ((chunk ^ sw_b) << 4) + inb;
+    voffA[dt] = kPPStages * TILE + rowA * RB + ((chunk ^ sw_a) << 4) + inb;
+    voffB[dt] = kPPStages * TILE + (rowA + 8) * RB + ((chunk ^ sw_b) << 4) + inb;
   }
 
-  floatx16 oa[NT], ob[NT];
+  floatx16 oacc[NT];
 #pragma unroll
-  for (int dt = 0; dt < NT; ++dt) {
-    oa[dt] = floatx16{0};
-    ob[dt] = floatx16{0};
-  }
-  float m_a = -1e30f, m_b = -1e30f, l_a = 0.f, l_b = 0.f;
+  for (int dt = 0; dt < NT; ++dt) oacc[dt] = floatx16{0};
+  floatx16 s0 = floatx16{0}, s1 = floatx16{0};
+  v8 pb[4];
+#pragma unroll
+  for (int st = 0; st < 4; ++st) pb[st] = v8{};
+  float m_run = -1e30f;                  // running max of s*scale*log2(e)
+  float l4[4] = {0.f, 0.f, 0.f, 0.f};    // this lane's share of the row sum, 4 partials
   const float cs = p.scale_log2;
-  const int trow_a = 64 * wave + i32, trow_b = trow_a + 32;
+  const int my_tile_row = 32 * wave + i32;
 
-  // S^T of one block for both sub-tiles (K fragments shared).
-  auto qk = [&](const lds_char* ks, floatx16* sa, floatx16* sb) {
-    sa[0] = sa[1] = sb[0] = sb[1] = floatx16{0};
+  // M(j) with K of block j in stage STG and V of block j - 1 in stage STG - 1:
+  // S^T (2*ND MFMAs) then O^T += V^T P^T (4*NT MFMAs) as one stream whose LDS
+  // operands are read LA MFMAs ahead.
+  constexpr int LA = 4;
+  constexpr int NQK = 2 * ND, NM = NQK + 4 * NT;
+  auto mphase = [&](auto stg_c) __attribute__((always_inline)) {
+    constexpr int STG = decltype(stg_c)::value;
+    constexpr int VSTG = (STG + kPPStages - 1) & (kPPStages - 1);
+    v8 opa[NM];
+    s0 = floatx16{0};
+    s1 = floatx16{0};
 #pragma unroll
-    for (int c = 0; c < ND; ++c) {
-      const v8 k0f = *reinterpret_cast<const __attribute__((address_space(3))) v8*>(ks + koff[c]);
-      const v8 k1f = *reinterpret_cast<const __attribute__((address_space(3))) v8*>(ks + koff[c] + 32 * RB);
-      sa[0] = O::mfma(k0f, qa[c], sa[0]);
-      sb[0] = O::mfma(k0f, qb[c], sb[0]);
-      sa[1] = O::mfma(k1f, qa[c], sa[1]);
-      sb[1] = O::mfma(k1f, qb[c], sb[1]);
+    for (int i = -LA; i < NM; ++i) {
+      const int li = i + LA;
+      if (li < NM) {
+        if (li < NQK) {
+          opa[li] = *reinterpret_cast<const __attribute__((address_space(3))) v8*>(
+              smem + koff[li >> 1] + (li & 1) * 32 * RB + STG * TILE);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        } else {
+          const int k = li - NQK, st = k / NT, dt = k % NT;
+          const shortx4 ta = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) shortx4*)(smem + voffA[dt] + VSTG * TILE + 16 * st * RB));
+          const shortx4 tb = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) shortx4*)(smem + voffB[dt] + VSTG * TILE + 16 * st * RB));
+          opa[li] = __builtin_bit_cast(v8, shortx8{ta[0], ta[1], ta[2], ta[3], tb[0], tb[1], tb[2], tb[3]});
+          __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        }
+      }
+      if (i >= 0) {
+        if (i < NQK) {
+          if (i & 1) s1 = O::mfma(opa[i], qf[i >> 1], s1);
+          else s0 = O::mfma(opa[i], qf[i >> 1], s0);
+        } else {
+          const int k = i - NQK;
+          oacc[k % NT] = O::mfma(opa[i], pb[k / NT], oacc[k % NT]);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      }
     }
+    pin(s0);
+    pin(s1);
+#pragma unroll
+    for (int dt = 0; dt < NT; ++dt) pin(oacc[dt]);
   };
 
-  // Mask keep-bits of one sub-tile (bit r: register r%16 of key half r/16).
-  auto keep_bits = [&](uint32_t cx, uint32_t cy, int trow, int64_t row) -> uint32_t {
+  // S(j): masks, row max, lazy rescale, P = 2^(s*cs - m) packed for the
+  // next M phase, row sums.
+  auto sphase = [&](int j) __attribute__((always_inline)) {
+    advance(e0 + j);
+    uint32_t cx, cy;
+    entry(e0 + j, cx, cy);
+    // Bit r of `keep` covers register r%16 of key half r/16, which holds key
+    // 8q + jj + 4h of the block with q = r/4, jj = r%4.
     const uint32_t kind = cy & 3u;
-    if (kind == kKindTwoPart) {
-      const int bits = (cy >> 2) & 0xF;
-      const int kb = (int)((cy >> 8) & 0xFF) - 4 * h;
-      const int qs = (cy >> 16) & 0xFF;
-      const bool rb = trow >= qs;
-      const uint32_t lo_ok = (bits >> (rb ? 2 : 0)) & 1;
-      const uint32_t hi_ok = (bits >> (rb ? 3 : 1)) & 1;
-      int n_lo = 0;
+    if (kind != kKindNone) {
+      uint32_t keep;
+      if (kind == kKindTwoPart) {
+        const int bits = (cy >> 2) & 0xF;
+        const int kb = (int)((cy >> 8) & 0xFF) - 4 * h;
+        const int qs = (cy >> 16) & 0xFF;
+        const bool rb = my_tile_row >= qs;
+        const uint32_t lo_ok = (bits >> (rb ? 2 : 0)) & 1;
+        const uint32_t hi_ok = (bits >> (rb ? 3 : 1)) & 1;
+        int n_lo = 0;
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const int c = kb - 8 * q;
-        n_lo += c < 0 ? 0 : (c > 4 ? 4 : c);
+        for (int q = 0; q < 8; ++q) {
+          const int c = kb - 8 * q;
+          n_lo += c < 0 ? 0 : (c > 4 ? 4 : c);
+        }
+        const uint32_t lo_mask = n_lo >= 32 ? 0xFFFFFFFFu : ((1u << n_lo) - 1u);
+        keep = (lo_ok ? lo_mask : 0u) | (hi_ok ? ~lo_mask : 0u);
+      } else {
+        const bool extra = (cx >> 31) != 0;
+        const int64_t k0 = (int64_t)(cx & 0x7fffffffu) * kBN;
+        const int64_t nsrc = extra ? p.n_x : p.n_k;
+        const int64_t qtok = p.q_tok0 + (my_row < nrows ? my_row : (int64_t)nrows - 1);
+        const int qf_row = (int)(qtok / p.R) - p.q_frame0;
+        const uint32_t* relrow = p.rel + (int64_t)qf_row * p.words;
+        keep = 0;
+        for (int r = 0; r < 32; ++r) {
+          const int64_t key = k0 + 8 * (r >> 2) + 4 * h + (r & 3);
+          if (key < nsrc) {
+            const int64_t kf = (p.k_tok0 + key) / p.C;
+            if ((kf >> 5) < p.words && ((relrow[kf >> 5] >> (kf & 31)) & 1u)) keep |= 1u << r;
+          }
+        }
       }
-      const uint32_t lo_mask = n_lo >= 32 ? 0xFFFFFFFFu : ((1u << n_lo) - 1u);
-      return (lo_ok ? lo_mask : 0u) | (hi_ok ? ~lo_mask : 0u);
-    }
-    const bool extra = (cx >> 31) != 0;
-    const int64_t k0 = (int64_t)(cx & 0x7fffffffu) * kBN;
-    const int64_t nsrc = extra ? p.n_x : p.n_k;
-    const int64_t qtok = p.q_tok0 + (row < nrows ? row : (int64_t)nrows - 1);
-    const int qf_row = (int)(qtok / p.R) - p.q_frame0;
-    const uint32_t* relrow = p.rel + (int64_t)qf_row * p.words;
-    uint32_t keep = 0;
-    for (int r = 0; r < 32; ++r) {
-      const int64_t key = k0 + 8 * (r >> 2) + 4 * h + (r & 3);
-      if (key < nsrc) {
-        const int64_t kf = (p.k_tok0 + key) / p.C;
-        if ((kf >> 5) < p.words && ((relrow[kf >> 5] >> (kf & 31)) & 1u)) keep |= 1u << r;
-      }
-    }
-    return keep;
-  };
-
-  // Online softmax of one sub-tile: S (2 x 16 regs) -> packed P (4 x v8).
-  auto softmax = [&](floatx16* s, uint32_t cx, uint32_t cy, int trow, int64_t row, float& m_run, float& l_run,
-                     floatx16* oacc, v8* pk8) {
-    if ((cy & 3u) != kKindNone) {
-      const uint32_t keep = keep_bits(cx, cy, trow, row);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        s[0][r] = ((keep >> r) & 1u) ? s[0][r] : -INFINITY;
-        s[1][r] = ((keep >> (r + 16)) & 1u) ? s[1][r] : -INFINITY;
+        s0[r] = ((keep >> r) & 1u) ? s0[r] : -INFINITY;
+        s1[r] = ((keep >> (r + 16)) & 1u) ? s1[r] : -INFINITY;
       }
     }
-    float mx = fmaxf(fmaxf(s[0][0], s[0][1]), s[1][0]);
+
+    // block row max: four independent chains of v_maximum3, then the partner lane
+    float mc[4];
 #pragma unroll
-    for (int r = 2; r < 16; ++r) mx = fmaxf(fmaxf(mx, s[0][r]), s[1][r]);
-    mx = fmaxf(mx, s[1][1]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    for (int c = 0; c < 4; ++c) {
+      float m = vmax(s0[4 * c], s0[4 * c + 1]);
+      m = vmax(m, s0[4 * c + 2]);
+      m = vmax(m, s0[4 * c + 3]);
+      m = vmax(m, s1[4 * c]);
+      m = vmax(m, s1[4 * c + 1]);
+      m = vmax(m, s1[4 * c + 2]);
+      mc[c] = vmax(m, s1[4 * c + 3]);
+    }
+    const float mx = max_halves(vmax(vmax(mc[0], mc[1]), vmax(mc[2], mc[3])));
     const float mxs = mx * cs;
     if (__builtin_amdgcn_ballot_w64(mxs > m_run + 8.0f)) {
-      const float m_new = fmaxf(m_run, mxs);
+      const float m_new = vmax(m_run, mxs);
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-      l_run *= alpha;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) l4[i] *= alpha;
 #pragma unroll
       for (int dt = 0; dt < NT; ++dt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
       m_run = m_new;
     }
+
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
-      const floatx16& src = s[st >> 1];
+      const floatx16& src = (st < 2) ? s0 : s1;
       const int base = 8 * (st & 1);
       v2 pk[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float a = __builtin_amdgcn_exp2f(__builtin_fmaf(src[base + 2 * j], cs, -m_run));
-        const float b = __builtin_amdgcn_exp2f(__builtin_fmaf(src[base + 2 * j + 1], cs, -m_run));
-        pk[j] = O::pack(a, b);
-        l_run = O::dot2(pk[j], l_run);
+      for (int jj = 0; jj < 4; ++jj) {
+        const float a = __builtin_amdgcn_exp2f(__builtin_fmaf(src[base + 2 * jj], cs, -m_run));
+        const float b = __builtin_amdgcn_exp2f(__builtin_fmaf(src[base + 2 * jj + 1], cs, -m_run));
+        pk[jj] = O::pack(a, b);
+        l4[jj] = O::dot2(pk[jj], l4[jj]);
       }
-      pk8[st] = v8{pk[0][0], pk[0][1], pk[1][0], pk[1][1], pk[2][0], pk[2][1], pk[3][0], pk[3][1]};
+      pb[st] = v8{pk[0][0], pk[0][1], pk[1][0], pk[1][1], pk[2][0], pk[2][1], pk[3][0], pk[3][1]};
     }
+#pragma unroll
+    for (int st = 0; st < 4; ++st) pin(pb[st]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pin(l4[i]);
+    pin(m_run);
+#pragma unroll
+    for (int dt = 0; dt < NT; ++dt) pin(oacc[dt]);
   };
 
-  // O^T += V^T P^T for both sub-tiles (V fragments shared).
-  auto pv = [&](const lds_char* vs, const v8* pa8, const v8* pb8) {
+  // V tile of stage 3 = 0: read by the P V of block -1 in M(0) (with P = 0).
+  {
+    constexpr int NZ = TILE / (16 * kPPThreads);
 #pragma unroll
-    for (int st = 0; st < 4; ++st) {
-#pragma unroll
-      for (int dt = 0; dt < NT; ++dt) {
-        const shortx4 ta = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) shortx4*)(vs + voffA[dt] + 16 * st * RB));
-        const shortx4 tb = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) shortx4*)(vs + voffB[dt] + 16 * st * RB));
-        const v8 vf = __builtin_bit_cast(v8, shortx8{ta[0], ta[1], ta[2], ta[3], tb[0], tb[1], tb[2], tb[3]});
-        oa[dt] = O::mfma(vf, pa8[st], oa[dt]);
-        ob[dt] = O::mfma(vf, pb8[st], ob[dt]);
-      }
-    }
-  };
-
-  // Pipeline over the n blocks of the tile (stage of block j = j % 3):
-  //   iteration j:  S = K(j) Q^T;  O += P(j-1) V(j-1);  P(j) = softmax(S)
-  // so the softmax VALU of block j runs while the P V MFMAs of block j-1 are
-  // in the matrix pipe.  The DMA of block j+1 is issued at the top of
-  // iteration j, after the barrier that retires block j-2's stage.
-  const int n = e1 - e0;
-  floatx16 sa[2], sb[2];
-  v8 pa8[4], pb8[4];
-  uint32_t cx = 0, cy = 0;      // entry of block j
-  uint32_t nx = 0, ny = 0;      // entry of block j+1
-  if (n > 0) {
-    entry(e0, cx, cy);
-    issue(cx, 0);
-    if (n > 1) entry(e0 + 1, nx, ny);
+    for (int z = 0; z < NZ; ++z)
+      *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(
+          smem + (2 * kPPStages - 1) * TILE + (z * kPPThreads + (int)threadIdx.x) * 16) = u32x4{0, 0, 0, 0};
   }
-  for (int j = 0; j < n; ++j) {
-    const int stage = j % kStages2;
-    wait_vm0();          // block j has landed (the only DMA in flight)
-    __syncthreads();     // ... for every wave; block j-2's stage is retired
-    if (j + 1 < n) issue(nx, (j + 1) % kStages2);
-    qk(smem + stage * STAGE, sa, sb);
-    if (j > 0) pv(smem + ((j + kStages2 - 1) % kStages2) * STAGE + TILE, pa8, pb8);
-    softmax(sa, cx, cy, trow_a, row_a, m_a, l_a, oa, pa8);
-    softmax(sb, cx, cy, trow_b, row_b, m_b, l_b, ob, pb8);
-    cx = nx;
-    cy = ny;
-    if (j + 2 < n) entry(e0 + j + 2, nx, ny);
-  }
-  if (n > 0) pv(smem + ((n - 1) % kStages2) * STAGE + TILE, pa8, pb8);
+  __syncthreads();
 
-  // Epilogue for both sub-tiles.
-  auto store = [&](floatx16* oacc, float l_run, float m_run, int64_t row) {
-    const float l_tot = l_run + __shfl_xor(l_run, 32);
-    if (row < nrows) {
-      const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
-      char* op = obase + row * ors;
-#pragma unroll
-      for (int dt = 0; dt < NT; ++dt) {
-#pragma unroll
-        for (int rq = 0; rq < 4; ++rq) {
-          const int d0 = 32 * dt + 8 * rq + 4 * h;
-          uint2 pk;
-          pk.x = (uint32_t)O::bits(oacc[dt][4 * rq] * inv) | ((uint32_t)O::bits(oacc[dt][4 * rq + 1] * inv) << 16);
-          pk.y = (uint32_t)O::bits(oacc[dt][4 * rq + 2] * inv) | ((uint32_t)O::bits(oacc[dt][4 * rq + 3] * inv) << 16);
-          *reinterpret_cast<uint2*>(op + 2 * d0) = pk;
-        }
-      }
-      if (lse && h == 0) lse[row] = l_tot > 0.f ? (m_run + __log2f(l_tot)) * 0.69314718055994530942f : -INFINITY;
+  // Prologue: group 1 starts blocks 0 and 1; block 0 lands before phase 0.
+  if (grp == 1) {
+    uint32_t x, y;
+    if (n > 0) {
+      entry(e0, x, y);
+      issue(x, smem, smem + kPPStages * TILE);
     }
-  };
-  store(oa, l_a, m_a, row_a);
-  store(ob, l_b, m_b, row_b);
+    if (n > 1) {
+      entry(e0 + 1, x, y);
+      issue(x, smem + TILE, smem + (kPPStages + 1) * TILE);
+      wait_vm<2 * NIW>();
+    } else {
+      wait_vm<0>();
+    }
+  }
+  wg_barrier();
+
+  // Group 0 runs phases 0 .. 2n: M(j) on phase 2j, S(j) on phase 2j + 1.
+  // Group 1 runs them one phase later and owns the DMA: during S(j) (phase
+  // 2j + 2) it starts block j + 3, whose stage last held block j - 1, read
+  // for the last time by group 1's M(j) on phase 2j + 1.  Both groups pass
+  // 2n + 1 barriers.  Blocks are processed 4 at a time so the stage of every
+  // block is a compile-time constant.
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I3 = std::integral_constant<int, 3>;
+  if (grp == 0) {
+    for (int j0 = 0;; j0 += 4) {
+      mphase(I0{});
+      wg_barrier();
+      if (j0 >= n) break;
+      sphase(j0);
+      wg_barrier();
+      mphase(I1{});
+      wg_barrier();
+      if (j0 + 1 >= n) break;
+      sphase(j0 + 1);
+      wg_barrier();
+      mphase(I2{});
+      wg_barrier();
+      if (j0 + 2 >= n) break;
+      sphase(j0 + 2);
+      wg_barrier();
+      mphase(I3{});
+      wg_barrier();
+      if (j0 + 3 >= n) break;
+      sphase(j0 + 3);
+      wg_barrier();
+    }
+  } else {
+    // block j + 1 is read from the phase after M(j) on; only block j + 2 may
+    // still be in flight
+    auto land = [&](int j) __attribute__((always_inline)) {
+      if (j + 2 < n) wait_vm<2 * NIW>();
+      else wait_vm<0>();
+    };
+    auto start = [&](auto st_c, int b) __attribute__((always_inline)) {
+      constexpr int BST = decltype(st_c)::value;
+      if (b < n) {
+        uint32_t x, y;
+        entry(e0 + b, x, y);
+        issue(x, smem + BST * TILE, smem + (kPPStages + BST) * TILE);
+      }
+    };
+    start(I2{}, 2);
+    wg_barrier();
+    for (int j0 = 0;; j0 += 4) {
+      mphase(I0{});
+      land(j0);
+      if (j0 >= n) break;
+      wg_barrier();
+      sphase(j0);
+      start(I3{}, j0 + 3);
+      wg_barrier();
+      mphase(I1{});
+      land(j0 + 1);
+      if (j0 + 1 >= n) break;
+      wg_barrier();
+      sphase(j0 + 1);
+      start(I0{}, j0 + 4);
+      wg_barrier();
+      mphase(I2{});
+      land(j0 + 2);
+      if (j0 + 2 >= n) break;
+      wg_barrier();
+      sphase(j0 + 2);
+      start(I1{}, j0 + 5);
+      wg_barrier();
+      mphase(I3{});
+      land(j0 + 3);
+      if (j0 + 3 >= n) break;
+      wg_barrier();
+      sphase(j0 + 3);
+      start(I2{}, j0 + 6);
+      wg_barrier();
+    }
+  }
+
+  // Epilogue: combine the row sum of both halves, normalise, store.
+  const float l_run = (l4[0] + l4[1]) + (l4[2] + l4[3]);
+  const float l_tot = sum_halves(l_run);
+  if (my_row < nrows) {
+    const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+    char* op = obase + my_row * ors;
+#pragma unroll
+    for (int dt = 0; dt < NT; ++dt) {
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq) {
+        const int d0 = 32 * dt + 8 * rq + 4 * h;
+        uint2 pk;
+        pk.x = (uint32_t)O::bits(oacc[dt][4 * rq] * inv) | ((uint32_t)O::bits(oacc[dt][4 * rq + 1] * inv) << 16);
+        pk.y = (uint32_t)O::bits(oacc[dt][4 * rq + 2] * inv) | ((uint32_t)O::bits(oacc[dt][4 * rq + 3] * inv) << 16);
+        *reinterpret_cast<uint2*>(op + 2 * d0) = pk;
+      }
+    }
+    if (lse && h == 0) {
+      lse[my_row] = l_tot > 0.f ? (m_run + __log2f(l_tot)) * 0.69314718055994530942f : -INFINITY;
+    }
+  }
 }
 
 template <int D, typename E>
 int launch(const AttnParams& prm, int block_q, hipStream_t stream) {
-  if (block_q == kBM2) {
-    hipLaunchKernelGGL((attn_fwd_v2_kernel<D, E>), dim3(prm.total_work), dim3(kThreads), 0, stream, prm);
+  if (block_q == kPPBM) {
+    hipLaunchKernelGGL((attn_fwd_pp_kernel<D, E>), dim3(prm.total_work), dim3(kPPThreads), 0, stream, prm);
   } else {
     hipLaunchKernelGGL((attn_fwd_kernel<D, E>), dim3(prm.total_work), dim3(kThreads), 0, stream, prm);
   }
@@ -848,7 +1050,7 @@ extern "C" int lvsa_attn_fwd(const lvsa_attn_args* a, hipStream_t stream) {
   LVSA_REQUIRE(a->n_q >= 0 && a->n_k >= 0 && a->n_x >= 0 && a->n_tq >= 0, LVSA_ERR_INVALID_ARG,
                "lvsa_attn_fwd: negative length");
   LVSA_REQUIRE(a->tile_indptr && a->entries, LVSA_ERR_INVALID_ARG, "lvsa_attn_fwd: missing plan");
-  LVSA_REQUIRE(a->block_q == kBM || a->block_q == kBM2, LVSA_ERR_UNSUPPORTED,
+  LVSA_REQUIRE(a->block_q == kBM || a->block_q == kPPBM, LVSA_ERR_UNSUPPORTED,
                "lvsa_attn_fwd: block_q %d (the kernels tile 128 or 256 query rows)", a->block_q);
   const int n_vt = (int)ceil_div(a->n_q, a->block_q), n_tt = (int)ceil_div(a->n_tq, a->block_q);
   LVSA_REQUIRE(a->n_video_tiles == n_vt && a->n_tiles == n_vt + n_tt, LVSA_ERR_INVALID_ARG,

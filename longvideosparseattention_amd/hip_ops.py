@@ -21,9 +21,17 @@ _DTYPES = {torch.bfloat16: capi.LVSA_BF16, torch.float16: capi.LVSA_FP16}
 SUPPORTED_HEAD_DIMS = (64, 128)
 
 
-def attn_block_q() -> int:
-    """Query rows per attention tile: 256 (64 rows per wave, pipelined) or 128."""
-    return int(os.environ.get("LVSA_ATTN_BLOCK_Q", "128"))
+def attn_block_q(head_dim: int = 128) -> int:
+    """Query rows per attention tile, i.e. which kernel a plan is built for.
+
+    256 for head_dim 128: the 8-wave kernel whose two wave groups alternate
+    MFMA and softmax phases.  128 for head_dim 64: with half the MFMA work per
+    softmax, the alternating phases become VALU-bound and the 4-wave kernel
+    is faster.  ``LVSA_ATTN_BLOCK_Q`` (128 or 256) overrides the choice."""
+    env = os.environ.get("LVSA_ATTN_BLOCK_Q")
+    if env:
+        return int(env)
+    return 256 if head_dim == 128 else 128
 
 
 def _stream(device: torch.device) -> int:
@@ -141,8 +149,11 @@ class BlockPlan:
 def plan_build(rel: Optional[torch.Tensor], *, n_q: int, n_k: int, n_x: int = 0, n_tq: int = 0,
                R: int = 1, Cf: int = 1, q_tok0: int = 0, k_tok0: int = 0, q_frame0: int = 0,
                max_row_frames: int = 0, block_q: Optional[int] = None, block_k: int = capi.ATTN_BLOCK_K,
-               device: Optional[torch.device] = None) -> BlockPlan:
-    """Refine a frame relation (bitmap rows x words, int32) to token blocks."""
+               head_dim: int = 128, device: Optional[torch.device] = None) -> BlockPlan:
+    """Refine a frame relation (bitmap rows x words, int32) to token blocks.
+
+    ``block_q`` defaults to the tile height of the kernel that serves
+    ``head_dim`` (see :func:`attn_block_q`)."""
     if rel is not None:
         _require_device(rel, "relation bitmap")
         device = rel.device
@@ -151,7 +162,7 @@ def plan_build(rel: Optional[torch.Tensor], *, n_q: int, n_k: int, n_x: int = 0,
         raise RuntimeError("lvsa_plan_build runs on the GPU only")
     device = torch.device(device)
     if block_q is None:
-        block_q = attn_block_q()
+        block_q = attn_block_q(head_dim)
     p = capi.PlanParams()
     p.n_q, p.n_k, p.n_x, p.n_tq = n_q, n_k, n_x, n_tq
     p.R, p.C = R, Cf

@@ -435,34 +435,37 @@ class LVSAMetadata:
 
     # ── Block plans (cached per device and call geometry) ──
 
-    def window_plan(self, device: torch.device, n_q: int, n_k: int, n_extra: int) -> hip_ops.BlockPlan:
+    def window_plan(self, device: torch.device, n_q: int, n_k: int, n_extra: int,
+                    head_dim: int = 128) -> hip_ops.BlockPlan:
         """Plan for ``lvsa_sdpa`` semantics: every query row attends all extra
         rows (``k_global``) plus the non-global window frames of its frame."""
         st = self.device_state(device)
-        key = ("window", n_q, n_k, n_extra)
+        block_q = hip_ops.attn_block_q(head_dim)
+        key = ("window", n_q, n_k, n_extra, block_q)
         plan = st.plans.get(key)
         if plan is None:
             P, gts = self.num_patches, self.global_token_start
             plan = hip_ops.plan_build(
                 st.mask.rel_window, n_q=n_q, n_k=n_k, n_x=n_extra, R=P, Cf=P, q_tok0=gts, k_tok0=gts,
-                q_frame0=gts // P, max_row_frames=max(1, 2 * self.window_size + 1))
+                q_frame0=gts // P, max_row_frames=max(1, 2 * self.window_size + 1), block_q=block_q)
             st.plans[key] = plan
         return plan
 
-    def full_plan(self, device: torch.device, n_q: int, n_k: int, n_text_k: int, n_text_q: int
-                  ) -> hip_ops.BlockPlan:
+    def full_plan(self, device: torch.device, n_q: int, n_k: int, n_text_k: int, n_text_q: int,
+                  head_dim: int = 128) -> hip_ops.BlockPlan:
         """Zero-copy plan: query rows attend their global + window frames of
         ``key`` directly, all text keys, and text queries attend everything."""
         if self.world != 1:
             raise NotImplementedError("zero-copy LVSA attention needs the whole sequence on one GPU (world=1)")
         st = self.device_state(device)
-        key = ("full", n_q, n_k, n_text_k, n_text_q)
+        block_q = hip_ops.attn_block_q(head_dim)
+        key = ("full", n_q, n_k, n_text_k, n_text_q, block_q)
         plan = st.plans.get(key)
         if plan is None:
             P = self.num_patches
             plan = hip_ops.plan_build(
                 st.mask.rel_full, n_q=n_q, n_k=n_k, n_x=n_text_k, n_tq=n_text_q, R=P, Cf=P,
-                max_row_frames=max(1, self.max_row_frames))
+                max_row_frames=max(1, self.max_row_frames), block_q=block_q)
             st.plans[key] = plan
         return plan
 
@@ -506,7 +509,7 @@ def lvsa_sdpa(
     """
     hip_ops._require_device(query, "query")
     dt = _compute_dtype(query)
-    plan = metadata.window_plan(query.device, query.shape[1], key.shape[1], k_global.shape[1])
+    plan = metadata.window_plan(query.device, query.shape[1], key.shape[1], k_global.shape[1], query.shape[-1])
     q, k, v, kg, vg = (x if x.dtype == dt else x.to(dt) for x in (query, key, value, k_global, v_global))
     out, _, _, _ = hip_ops.attn_fwd(q, k, v, plan, kx=kg, vx=vg)
     return out if out.dtype == query.dtype else out.to(query.dtype)
@@ -591,7 +594,7 @@ def lvsa_attention(
     dt = _compute_dtype(query)
     n_tk = 0 if k_text is None else k_text.shape[1]
     n_tq = 0 if q_text is None else q_text.shape[1]
-    plan = metadata.full_plan(query.device, query.shape[1], key.shape[1], n_tk, n_tq)
+    plan = metadata.full_plan(query.device, query.shape[1], key.shape[1], n_tk, n_tq, query.shape[-1])
     cast = lambda x: x if (x is None or x.dtype == dt) else x.to(dt)  # noqa: E731
     out, out_t, lse, lse_t = hip_ops.attn_fwd(
         cast(query), cast(key), cast(value), plan, kx=cast(k_text), vx=cast(v_text), qt=cast(q_text),

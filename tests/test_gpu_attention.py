@@ -59,8 +59,12 @@ SMALL = [
 ]
 
 
+@pytest.mark.parametrize("block_q", [128, 256], ids=["tile128", "tile256"])
 @pytest.mark.parametrize("cfg", SMALL, ids=[str(c[:10]) for c in SMALL])
-def test_fused_attention_small(cfg, gpu):
+def test_fused_attention_small(cfg, block_q, gpu, monkeypatch):
+    """Both kernels (128-row tiles: 4 waves; 256-row tiles: 8 waves in two
+    alternating groups) on every small configuration."""
+    monkeypatch.setenv("LVSA_ATTN_BLOCK_Q", str(block_q))
     T, P, W, n, kfi, off, H, Hkv, D, n_txt, dt = cfg
     N = T * P
     m = _meta(T, P, W, n, kfi, off)
