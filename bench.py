@@ -60,7 +60,22 @@ def parse(argv=None):
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-baseline sample budget")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="instead of the benchmark, copy a MIB-MiB device buffer 4 times (one kernel each): "
+                         "the known-size reference that scales rocprof FETCH_SIZE / WRITE_SIZE to bytes")
     return ap.parse_args(argv)
+
+
+def copy_calibration(mib: int) -> int:
+    """Plain device-to-device copies of a known size, for counter calibration."""
+    n = mib << 20
+    x = torch.ones(n, dtype=torch.uint8, device="cuda")
+    y = torch.empty_like(x)
+    for _ in range(4):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes_read": n, "copy_calibration_bytes_written": n, "launches": 4}))
+    return 0
 
 
 def cpu_baseline(q, k, v, qt, kt, vt, meta, budget_s: float):
@@ -104,8 +119,10 @@ def main(argv=None) -> int:
     args = parse(argv)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs the LVSA hot path on ONE GPU; multi-GPU runs are not part of it "
-              "(see DESIGN.md for how the path would shard).", file=sys.stderr)
+              "(the design notes describe how the path would shard over heads).", file=sys.stderr)
         return 2
+    if args.copy_calibration:
+        return copy_calibration(args.copy_calibration)
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
         return 1

@@ -127,6 +127,26 @@ __device__ __forceinline__ void dma16(const void* g, lds_char* l) {
   __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)l, 16, 0, 0);
 }
 
+// The same copy issued as inline asm.  The compiler does not see the LDS
+// write, so it inserts no vmcnt wait before later LDS reads it cannot prove
+// disjoint (it cannot for the ring stages, and such a wait makes every copy
+// synchronous); the kernel orders the copies itself with explicit vmcnt
+// waits and barriers.  The addresses are made uniform so both land in SGPRs;
+// the s_nop covers the M0-write -> LDS-DMA hazard.  Nothing else in a kernel
+// that uses this may rely on M0.
+__device__ __forceinline__ void dma16_async(const char* g, uint32_t voff, const lds_char* l) {
+  // readfirstlane returns int: go through uint32_t so nothing sign-extends
+  const uint64_t b = (uint64_t)g;
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32));
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b);
+  const uint64_t sb = ((uint64_t)hi << 32) | (uint64_t)lo;
+  const uint32_t la = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)l);
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(sb), "s"(la) : "m0");
+#pragma clang diagnostic pop
+}
+
 __device__ __forceinline__ void wait_vm0() {
   // s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima).
   __builtin_amdgcn_s_waitcnt(0x0F70);
@@ -482,8 +502,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
 // S(j): mask, row max, exp and row sums of block j (VALU).  At every phase
 // each SIMD runs one wave's MFMAs under the other wave's softmax.  K/V blocks
 // rotate through a 4-stage LDS ring: block b is read from phase 2b (S^T,
-// group 0) to phase 2b + 3 (P V, group 1), and group 1 DMAs block m + 2
-// during its softmax phase 2m, about three phases before its first use.
+// group 0) to phase 2b + 3 (P V, group 1), and group 0 DMAs block j + 2 from
+// its MFMA phase 2j, about three phases before its first use.
 // The four K tiles sit at [0, 4 TILE) and the four V tiles above them, and
 // the phase loop is unrolled over 8 phases so every stage is a compile-time
 // constant: each LDS read is a VGPR plus an immediate.  M phases are
@@ -667,37 +687,37 @@ __global__ __launch_bounds__(kPPThreads, 1) void attn_fwd_pp_kernel(AttnParams p
     }
   };
 
-  auto issue = [&](uint32_t ex, lds_char* ks, lds_char* vs) __attribute__((always_inline)) {
+  // DMA of one block as 2*NIW single instructions that the MFMA phase
+  // interleaves with its MFMAs: instruction 2*ii (+1) copies 1 KiB of K (V)
+  // rows RPI*(dw*NIW + ii) + lane/NCH, clamped to the last row of the source
+  // (rows past its end are masked by the plan).
+  struct BlockSrc {
+    const char* kb;
+    const char* vb;
+    uint32_t krs, vrs, lim;
+  };
+  auto prep = [&](uint32_t ex) __attribute__((always_inline)) {
     const bool extra = (ex >> 31) != 0;
     const int64_t nsrc = extra ? p.n_x : p.n_k;
     int64_t k0 = (int64_t)(ex & 0x7fffffffu) * kBN;
     if (k0 >= nsrc) k0 = 0;  // never produced by the plan; keeps every DMA in bounds
-    const uint32_t krs = extra ? krs1 : krs0, vrs = extra ? vrs1 : vrs0;
-    const char* kb = (extra ? kb1 : kb0) + k0 * krs;
-    const char* vb = (extra ? vb1 : vb0) + k0 * vrs;
-    if (k0 + kBN <= nsrc) {
-      const uint32_t lk = dma_lr * krs, lv = dma_lr * vrs;
-#pragma unroll
-      for (int ii = 0; ii < NIW; ++ii) {
-        const uint32_t row0 = (uint32_t)(RPI * (dw * NIW + ii));
-        const uint32_t c16 = dma_c16 ^ (uint32_t)(16 * (ii & (D == 128 ? 3 : 1)));
-        const int off = (dw * NIW + ii) * 1024;
-        dma16(kb + row0 * krs + (lk + c16), ks + off);
-        dma16(vb + row0 * vrs + (lv + c16), vs + off);
-      }
-    } else {
-      // last block of a source: rows past its end re-read the last row (masked later)
-      const uint32_t lim = (uint32_t)(nsrc - 1 - k0);
-#pragma unroll
-      for (int ii = 0; ii < NIW; ++ii) {
-        uint32_t r = (uint32_t)(RPI * (dw * NIW + ii)) + dma_lr;
-        r = r < lim ? r : lim;
-        const uint32_t c16 = dma_c16 ^ (uint32_t)(16 * (ii & (D == 128 ? 3 : 1)));
-        const int off = (dw * NIW + ii) * 1024;
-        dma16(kb + (r * krs + c16), ks + off);
-        dma16(vb + (r * vrs + c16), vs + off);
-      }
-    }
+    BlockSrc src;
+    src.krs = extra ? krs1 : krs0;
+    src.vrs = extra ? vrs1 : vrs0;
+    src.kb = (extra ? kb1 : kb0) + k0 * src.krs;
+    src.vb = (extra ? vb1 : vb0) + k0 * src.vrs;
+    const int64_t last = nsrc - 1 - k0;
+    src.lim = (uint32_t)(last < kBN - 1 ? last : kBN - 1);
+    return src;
+  };
+  auto dma_one = [&](const BlockSrc& src, int bst, int k) __attribute__((always_inline)) {
+    const int ii = k >> 1;
+    uint32_t r = (uint32_t)(RPI * (dw * NIW + ii)) + dma_lr;
+    r = r < src.lim ? r : src.lim;
+    const uint32_t c16 = dma_c16 ^ (uint32_t)(16 * (ii & (D == 128 ? 3 : 1)));
+    const int off = (dw * NIW + ii) * 1024;
+    if (k & 1) dma16_async(src.vb, __umul24(r, src.vrs) + c16, smem + (kPPStages + bst) * TILE + off);
+    else dma16_async(src.kb, __umul24(r, src.krs) + c16, smem + bst * TILE + off);
   };
 
   // Q fragments (B operand of S^T = K Q^T): row i32 of this wave, d = 16c + 8h .. +7.
@@ -745,7 +765,7 @@ __global__ __launch_bounds__(kPPThreads, 1) void attn_fwd_pp_kernel(AttnParams p
   // operands are read LA MFMAs ahead.
   constexpr int LA = 4;
   constexpr int NQK = 2 * ND, NM = NQK + 4 * NT;
-  auto mphase = [&](auto stg_c) __attribute__((always_inline)) {
+  auto mphase = [&](auto stg_c, auto&& after_mfma) __attribute__((always_inline)) {
     constexpr int STG = decltype(stg_c)::value;
     constexpr int VSTG = (STG + kPPStages - 1) & (kPPStages - 1);
     v8 opa[NM];
@@ -778,6 +798,7 @@ __global__ __launch_bounds__(kPPThreads, 1) void attn_fwd_pp_kernel(AttnParams p
           oacc[k % NT] = O::mfma(opa[i], pb[k / NT], oacc[k % NT]);
         }
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        after_mfma(i);
       }
     }
     pin(s0);
@@ -894,101 +915,102 @@ __global__ __launch_bounds__(kPPThreads, 1) void attn_fwd_pp_kernel(AttnParams p
   }
   __syncthreads();
 
-  // Prologue: group 1 starts blocks 0 and 1; block 0 lands before phase 0.
-  if (grp == 1) {
-    uint32_t x, y;
-    if (n > 0) {
-      entry(e0, x, y);
-      issue(x, smem, smem + kPPStages * TILE);
-    }
-    if (n > 1) {
-      entry(e0 + 1, x, y);
-      issue(x, smem + TILE, smem + (kPPStages + 1) * TILE);
-      wait_vm<2 * NIW>();
-    } else {
-      wait_vm<0>();
-    }
+  // Block b of the plan, or a stand-in past the end: row 0 of a key source,
+  // DMA'd into a stage that is never read again (keeps every MFMA phase the
+  // same instruction stream and the DMA count per phase constant).
+  const uint32_t stand_in = p.n_k > 0 ? 0u : 0x80000000u;
+  auto block_src = [&](int b) __attribute__((always_inline)) {
+    uint32_t x = stand_in, y;
+    if (b < n) entry(e0 + b, x, y);
+    return prep(x);
+  };
+
+  // Prologue: group 0 starts blocks 0 and 1; block 0 lands before phase 0.
+  if (grp == 0) {
+    const BlockSrc s0b = block_src(0);
+#pragma unroll
+    for (int k = 0; k < 2 * NIW; ++k) dma_one(s0b, 0, k);
+    const BlockSrc s1b = block_src(1);
+#pragma unroll
+    for (int k = 0; k < 2 * NIW; ++k) dma_one(s1b, 1, k);
+    wait_vm<2 * NIW>();
   }
   wg_barrier();
 
-  // Group 0 runs phases 0 .. 2n: M(j) on phase 2j, S(j) on phase 2j + 1.
-  // Group 1 runs them one phase later and owns the DMA: during S(j) (phase
-  // 2j + 2) it starts block j + 3, whose stage last held block j - 1, read
-  // for the last time by group 1's M(j) on phase 2j + 1.  Both groups pass
-  // 2n + 1 barriers.  Blocks are processed 4 at a time so the stage of every
-  // block is a compile-time constant.
+  // Group 0 runs phases 0 .. 2n: M(j) on phase 2j, S(j) on phase 2j + 1;
+  // group 1 runs them one phase later.  Both pass 2n + 1 barriers.  Group 0
+  // owns the DMA and spreads it over its MFMA phases (one instruction after
+  // every fourth MFMA): M(j) copies block j + 2, whose stage last held block
+  // j - 2 (read for the last time by group 1's M(j - 1) on phase 2j - 1), and
+  // S(j) ends with block j + 1 landed for M(j + 1) (only block j + 2 may
+  // still be in flight).  Blocks are processed 4 at a time so the stage of
+  // every block is a compile-time constant.
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
   using I2 = std::integral_constant<int, 2>;
   using I3 = std::integral_constant<int, 3>;
+  static_assert(2 * NIW * 4 <= NM, "one DMA instruction per four MFMAs");
   if (grp == 0) {
+    auto mdma = [&](auto stg_c, int b) __attribute__((always_inline)) {
+      constexpr int BST = (decltype(stg_c)::value + 2) & (kPPStages - 1);
+      const BlockSrc src = block_src(b);
+      mphase(stg_c, [&](int i) __attribute__((always_inline)) {
+        if ((i & 3) == 1 && (i >> 2) < 2 * NIW) {
+          dma_one(src, BST, i >> 2);
+          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+        }
+      });
+    };
     for (int j0 = 0;; j0 += 4) {
-      mphase(I0{});
+      mdma(I0{}, j0 + 2);
       wg_barrier();
       if (j0 >= n) break;
       sphase(j0);
+      wait_vm<2 * NIW>();
       wg_barrier();
-      mphase(I1{});
+      mdma(I1{}, j0 + 3);
       wg_barrier();
       if (j0 + 1 >= n) break;
       sphase(j0 + 1);
+      wait_vm<2 * NIW>();
       wg_barrier();
-      mphase(I2{});
+      mdma(I2{}, j0 + 4);
       wg_barrier();
       if (j0 + 2 >= n) break;
       sphase(j0 + 2);
+      wait_vm<2 * NIW>();
       wg_barrier();
-      mphase(I3{});
+      mdma(I3{}, j0 + 5);
       wg_barrier();
       if (j0 + 3 >= n) break;
       sphase(j0 + 3);
+      wait_vm<2 * NIW>();
       wg_barrier();
     }
+    wait_vm<0>();  // stand-in copies still in flight land before the workgroup ends
   } else {
-    // block j + 1 is read from the phase after M(j) on; only block j + 2 may
-    // still be in flight
-    auto land = [&](int j) __attribute__((always_inline)) {
-      if (j + 2 < n) wait_vm<2 * NIW>();
-      else wait_vm<0>();
-    };
-    auto start = [&](auto st_c, int b) __attribute__((always_inline)) {
-      constexpr int BST = decltype(st_c)::value;
-      if (b < n) {
-        uint32_t x, y;
-        entry(e0 + b, x, y);
-        issue(x, smem + BST * TILE, smem + (kPPStages + BST) * TILE);
-      }
-    };
-    start(I2{}, 2);
+    auto none = [](int) {};
     wg_barrier();
     for (int j0 = 0;; j0 += 4) {
-      mphase(I0{});
-      land(j0);
+      mphase(I0{}, none);
       if (j0 >= n) break;
       wg_barrier();
       sphase(j0);
-      start(I3{}, j0 + 3);
       wg_barrier();
-      mphase(I1{});
-      land(j0 + 1);
+      mphase(I1{}, none);
       if (j0 + 1 >= n) break;
       wg_barrier();
       sphase(j0 + 1);
-      start(I0{}, j0 + 4);
       wg_barrier();
-      mphase(I2{});
-      land(j0 + 2);
+      mphase(I2{}, none);
       if (j0 + 2 >= n) break;
       wg_barrier();
       sphase(j0 + 2);
-      start(I1{}, j0 + 5);
       wg_barrier();
-      mphase(I3{});
-      land(j0 + 3);
+      mphase(I3{}, none);
       if (j0 + 3 >= n) break;
       wg_barrier();
       sphase(j0 + 3);
-      start(I2{}, j0 + 6);
       wg_barrier();
     }
   }
@@ -1071,6 +1093,11 @@ extern "C" int lvsa_attn_fwd(const lvsa_attn_args* a, hipStream_t stream) {
   auto fits = [&](int64_t row_elems) { return row_elems >= 0 && row_elems * 2 * (kBN - 1) + 2LL * a->D <= 0xFFFFFFFFLL; };
   LVSA_REQUIRE(fits(a->k_str[1]) && fits(a->v_str[1]) && (a->n_x == 0 || (fits(a->kx_str[1]) && fits(a->vx_str[1]))),
                LVSA_ERR_UNSUPPORTED, "lvsa_attn_fwd: key/value row stride too large");
+  // the 256-row kernel forms per-lane row offsets with 24-bit multiplies
+  auto fits24 = [&](int64_t row_elems) { return row_elems * 2 < (1LL << 24); };
+  LVSA_REQUIRE(a->block_q != kPPBM || (fits24(a->k_str[1]) && fits24(a->v_str[1]) &&
+                                       (a->n_x == 0 || (fits24(a->kx_str[1]) && fits24(a->vx_str[1])))),
+               LVSA_ERR_UNSUPPORTED, "lvsa_attn_fwd: key/value row stride of 16 MiB or more (block_q 256)");
   const int64_t work = (int64_t)a->n_tiles * a->H * a->B;
   LVSA_REQUIRE(work < (int64_t)INT32_MAX, LVSA_ERR_INVALID_ARG, "lvsa_attn_fwd: too much work");
   if (work == 0) return LVSA_OK;
