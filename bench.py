@@ -31,6 +31,7 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 import longvideosparseattention_amd as lv  # noqa: E402
+from longvideosparseattention_amd import hip_ops as lvops  # noqa: E402
 from longvideosparseattention_amd import flops as lvflops  # noqa: E402
 
 MFMA_BF16_PEAK_TFLOPS = 2500.0
@@ -76,6 +77,21 @@ def copy_calibration(mib: int) -> int:
     torch.cuda.synchronize()
     print(json.dumps({"copy_calibration_bytes_read": n, "copy_calibration_bytes_written": n, "launches": 4}))
     return 0
+
+
+def profiled_traffic(config: str):
+    """HBM bytes per attention launch for `config`, as measured by the two
+    rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE, each scaled by the same
+    counter on a 1 GiB copy) summarised under profiles/; None if absent."""
+    import glob
+    import re
+
+    for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "*_counters.md"))):
+        with open(path) as f:
+            m = re.search(r"traffic_bytes_per_launch\[" + re.escape(config) + r"\]\s*=\s*(\d+)", f.read())
+        if m:
+            return int(m.group(1)), os.path.relpath(path, ROOT)
+    return None, None
 
 
 def cpu_baseline(q, k, v, qt, kt, vt, meta, budget_s: float):
@@ -180,6 +196,8 @@ def main(argv=None) -> int:
     value = fb / wall / 1e12
     achieved = fb / (ev_ms * 1e-3 * args.steps) / 1e12
     bytes_per_call = 4 * (N + n_text) * H * D * 2
+    traffic, traffic_src = profiled_traffic(args.config)
+    kernel = "attn_fwd_pp_kernel" if lvops.attn_block_q(D) == 256 else "attn_fwd_kernel"
 
     line = {
         "metric": "block-sparse attn ms/call + effective TFLOP/s (% bf16 MFMA peak), "
@@ -204,8 +222,8 @@ def main(argv=None) -> int:
         "hbm_gbs_algorithmic": round(bytes_per_call / (ms * 1e-3) / 1e9, 1),
         "mask_and_plan_build_ms": round(sum(build_ms) / len(build_ms), 3),
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
-                     "kernel": "attn_fwd_kernel", "kernel_ms": round(ev_ms, 4)},
+                     "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": traffic,
+                     "traffic_source": traffic_src, "kernel": kernel, "kernel_ms": round(ev_ms, 4)},
     }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(q.float().cpu(), k.float().cpu(), v.float().cpu(),

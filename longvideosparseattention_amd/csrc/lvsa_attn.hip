@@ -147,6 +147,19 @@ __device__ __forceinline__ void dma16_async(const char* g, uint32_t voff, const 
 #pragma clang diagnostic pop
 }
 
+// 16 bytes per lane, global -> LDS, through a buffer resource: lanes whose
+// soffset + voffset + 16 exceed the resource's num_records read zeros (per
+// dword) and write them to LDS, with no memory access.  Issued as asm for
+// the same reason as dma16_async.
+__device__ __forceinline__ void dma16_buf(u32x4 rsrc, uint32_t voff, uint32_t soff, const lds_char* l) {
+  const uint32_t la = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)l);
+  const uint32_t so = (uint32_t)__builtin_amdgcn_readfirstlane((int)soff);
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+  asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" : : "v"(voff), "s"(rsrc), "s"(so), "s"(la) : "m0");
+#pragma clang diagnostic pop
+}
+
 __device__ __forceinline__ void wait_vm0() {
   // s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima).
   __builtin_amdgcn_s_waitcnt(0x0F70);
@@ -634,18 +647,14 @@ __global__ __launch_bounds__(kPPThreads, 1) void attn_fwd_pp_kernel(AttnParams p
   const uint32_t krs0 = (uint32_t)(2 * p.k_str[1]), vrs0 = (uint32_t)(2 * p.v_str[1]);
   const uint32_t krs1 = (uint32_t)(2 * p.kx_str[1]), vrs1 = (uint32_t)(2 * p.vx_str[1]);
 
-  // DMA geometry of a group-1 wave: instruction ii fills LDS bytes
-  // [(dw*NIW + ii) KiB, +1 KiB) of a tile, i.e. block rows
-  // RPI*(dw*NIW + ii) + lane/NCH, physical chunk lane%NCH.  dw*NIW is a
-  // multiple of 4 (D=128) or 2 (D=64), so the swizzle of those rows is
-  // dma_c ^ ii with a per-lane dma_c.
-  const uint32_t dma_lr = (uint32_t)(lane / NCH);
-  uint32_t dma_c16;
-  if constexpr (D == 128) {
-    dma_c16 = (uint32_t)(((lane & 15) ^ ((lane >> 4) << 2)) * 16);
-  } else {
-    dma_c16 = (uint32_t)(((lane & 7) ^ ((((lane >> 4) & 1) << 2) | (((lane >> 5) & 1) << 1))) * 16);
-  }
+  // DMA geometry of a group-0 wave: instruction ii fills LDS KiB 4*ii + dw
+  // of a tile, i.e. block rows (4*ii + dw)*RPI + lane/NCH at physical chunk
+  // lane%NCH.  The swizzle of those rows depends on row & 15 = (dw*RPI +
+  // lane/NCH) & 15 only, so a lane's byte offset within the block is the
+  // same for every instruction of the wave and the instruction adds the
+  // uniform 4*ii*RPI rows as the buffer soffset.
+  const uint32_t dma_row = (uint32_t)(dw * RPI + lane / NCH);  // row of instruction 0
+  const uint32_t dma_c16 = (uint32_t)(((lane % NCH) ^ swz<D>((int)(dma_row & 15))) * 16);
 
   // Plan entries, 64 per VGPR batch (lane i holds entry eb + i) with the
   // following batch prefetched; a uniform entry is read with v_readlane.
@@ -689,12 +698,15 @@ __global__ __launch_bounds__(kPPThreads, 1) void attn_fwd_pp_kernel(AttnParams p
 
   // DMA of one block as 2*NIW single instructions that the MFMA phase
   // interleaves with its MFMAs: instruction 2*ii (+1) copies 1 KiB of K (V)
-  // rows RPI*(dw*NIW + ii) + lane/NCH, clamped to the last row of the source
-  // (rows past its end are masked by the plan).
+  // through a buffer resource that starts at the block's first row and ends
+  // after its last row inside the source, so the rows of a source's short
+  // last block past its end land as zeros (they are masked by the plan).
+  const uint32_t dofk0 = __umul24(dma_row, krs0) + dma_c16;
+  const uint32_t dofv0 = __umul24(dma_row, vrs0) + dma_c16;
   struct BlockSrc {
-    const char* kb;
-    const char* vb;
-    uint32_t krs, vrs, lim;
+    u32x4 kr, vr;          // buffer resources of the block's K and V rows
+    uint32_t krs, vrs;     // row strides (bytes)
+    uint32_t dk, dv;       // per-lane offsets
   };
   auto prep = [&](uint32_t ex) __attribute__((always_inline)) {
     const bool extra = (ex >> 31) != 0;
@@ -704,20 +716,21 @@ __global__ __launch_bounds__(kPPThreads, 1) void attn_fwd_pp_kernel(AttnParams p
     BlockSrc src;
     src.krs = extra ? krs1 : krs0;
     src.vrs = extra ? vrs1 : vrs0;
-    src.kb = (extra ? kb1 : kb0) + k0 * src.krs;
-    src.vb = (extra ? vb1 : vb0) + k0 * src.vrs;
-    const int64_t last = nsrc - 1 - k0;
-    src.lim = (uint32_t)(last < kBN - 1 ? last : kBN - 1);
+    const uint64_t kb = (uint64_t)((extra ? kb1 : kb0) + k0 * src.krs);
+    const uint64_t vb = (uint64_t)((extra ? vb1 : vb0) + k0 * src.vrs);
+    const int64_t rows = nsrc - k0 < kBN ? nsrc - k0 : kBN;
+    // resource words: base [47:0] (stride 0), num_records in bytes, raw 32-bit data format
+    src.kr = u32x4{(uint32_t)kb, (uint32_t)(kb >> 32) & 0xFFFFu, (uint32_t)(rows * src.krs), 0x00020000u};
+    src.vr = u32x4{(uint32_t)vb, (uint32_t)(vb >> 32) & 0xFFFFu, (uint32_t)(rows * src.vrs), 0x00020000u};
+    src.dk = extra ? __umul24(dma_row, krs1) + dma_c16 : dofk0;
+    src.dv = extra ? __umul24(dma_row, vrs1) + dma_c16 : dofv0;
     return src;
   };
   auto dma_one = [&](const BlockSrc& src, int bst, int k) __attribute__((always_inline)) {
     const int ii = k >> 1;
-    uint32_t r = (uint32_t)(RPI * (dw * NIW + ii)) + dma_lr;
-    r = r < src.lim ? r : src.lim;
-    const uint32_t c16 = dma_c16 ^ (uint32_t)(16 * (ii & (D == 128 ? 3 : 1)));
-    const int off = (dw * NIW + ii) * 1024;
-    if (k & 1) dma16_async(src.vb, __umul24(r, src.vrs) + c16, smem + (kPPStages + bst) * TILE + off);
-    else dma16_async(src.kb, __umul24(r, src.krs) + c16, smem + bst * TILE + off);
+    const uint32_t r = (uint32_t)(4 * ii * RPI);
+    if (k & 1) dma16_buf(src.vr, src.dv, r * src.vrs, smem + (kPPStages + bst) * TILE + (4 * ii + dw) * 1024);
+    else dma16_buf(src.kr, src.dk, r * src.krs, smem + bst * TILE + (4 * ii + dw) * 1024);
   };
 
   // Q fragments (B operand of S^T = K Q^T): row i32 of this wave, d = 16c + 8h .. +7.
@@ -728,6 +741,12 @@ __global__ __launch_bounds__(kPPThreads, 1) void attn_fwd_pp_kernel(AttnParams p
     const char* qp = qbase + qr * qrs + 16 * h;
 #pragma unroll
     for (int c = 0; c < ND; ++c) qf[c] = *reinterpret_cast<const v8*>(qp + 32 * c);
+    // Q lands here, once: re-defining the fragments through asm leaves no
+    // load the compiler would wait for inside the loop, where the hardware
+    // counter also counts the K/V copies in flight.
+    wait_vm<0>();
+#pragma unroll
+    for (int c = 0; c < ND; ++c) pin(qf[c]);
   }
 
   // LDS read offsets (relative to a stage).
