@@ -61,6 +61,8 @@ def parse(argv=None):
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-baseline sample budget")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--window", type=int, default=None,
+                    help="override the configuration's sliding window (the Wan 6x sweep uses 1, 2, 4)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="instead of the benchmark, copy a MIB-MiB device buffer 4 times (one kernel each): "
                          "the known-size reference that scales rocprof FETCH_SIZE / WRITE_SIZE to bytes")
@@ -144,6 +146,9 @@ def main(argv=None) -> int:
         return 1
     dev = torch.device("cuda", 0)
     T, P, H, D, W, kfi, offsets, n_text, block, workload = CONFIGS[args.config]
+    if args.window is not None:
+        W = args.window
+        workload += f", window +-{W}"
     N = T * P
     dt = torch.bfloat16
 
