@@ -114,9 +114,11 @@ struct Ops<_Float16> {
 //    the 4 rows of a transposing V read land in 4 distinct 64-byte quarters.
 //  D = 64 (8 chunks/row, 2 rows per bank line): a bijection on (r >> 1) & 7
 //    with bit 2 = (r >> 1) & 1 so rows r and r + 2 of a V read differ.
+//  D = 256 (32 chunks/row, a row spans the banks twice): the D = 128 swizzle on
+//    the low 4 chunk bits, which keeps both patterns inside one 256-byte half.
 template <int D>
 __device__ __forceinline__ int swz(int r) {
-  if constexpr (D == 128) {
+  if constexpr (D == 128 || D == 256) {
     return ((r & 3) << 2) | ((r >> 2) & 3);
   } else {
     return (((r >> 1) & 1) << 2) | (((r >> 2) & 1) << 1) | ((r >> 3) & 1);
@@ -166,7 +168,9 @@ __device__ __forceinline__ void wait_vm0() {
 }
 
 template <int D, typename E>
-__global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
+// Two work-groups per CU, except at D = 256 (its O and Q fragments alone take
+// 192 registers per lane): one work-group, registers up to 512.
+__global__ __launch_bounds__(kThreads, D == 256 ? 1 : 2) void attn_fwd_kernel(AttnParams p) {
   using O = Ops<E>;
   using v8 = typename O::v8;
   using v2 = typename O::v2;
@@ -242,13 +246,25 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
   // [(wave*NIW + ii) KiB, +1 KiB), i.e. block rows RPI*(wave*NIW + ii) + lane/NCH,
   // physical chunk lane%NCH.  Because wave*NIW is a multiple of 4 (D=128) or
   // 2 (D=64), the swizzle of those rows is  dma_c ^ ii  with a per-lane dma_c.
+  // (D = 256: two rows per instruction, the swizzle of instruction ii's
+  // rows is formed per instruction.)
   const uint32_t dma_lr = (uint32_t)(lane / NCH);
   uint32_t dma_c16;
   if constexpr (D == 128) {
     dma_c16 = (uint32_t)(((lane & 15) ^ ((lane >> 4) << 2)) * 16);
-  } else {
+  } else if constexpr (D == 64) {
     dma_c16 = (uint32_t)(((lane & 7) ^ ((((lane >> 4) & 1) << 2) | (((lane >> 5) & 1) << 1))) * 16);
+  } else {
+    dma_c16 = 0;
   }
+  auto c16_of = [&](int ii) __attribute__((always_inline)) {
+    if constexpr (D == 256) {
+      const uint32_t row = (uint32_t)(RPI * (wave * NIW + ii)) + dma_lr;
+      return (uint32_t)(((lane % NCH) ^ swz<D>((int)(row & 15))) * 16);
+    } else {
+      return dma_c16 ^ (uint32_t)(16 * (ii & (D == 128 ? 3 : 1)));
+    }
+  };
 
   // Plan entries of this tile, 64 at a time in a VGPR (lane i holds entry
   // base + i); a uniform entry is read with v_readlane.  The next batch is
@@ -280,7 +296,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
 #pragma unroll
       for (int ii = 0; ii < NIW; ++ii) {
         const uint32_t row0 = (uint32_t)(RPI * (wave * NIW + ii));
-        const uint32_t c16 = dma_c16 ^ (uint32_t)(16 * (ii & (D == 128 ? 3 : 1)));
+        const uint32_t c16 = c16_of(ii);
         const int off = (wave * NIW + ii) * 1024;
         dma16(kb + row0 * krs + (lk + c16), ks + off);
         dma16(vb + row0 * vrs + (lv + c16), vs + off);
@@ -292,7 +308,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
       for (int ii = 0; ii < NIW; ++ii) {
         uint32_t r = (uint32_t)(RPI * (wave * NIW + ii)) + dma_lr;
         r = r < lim ? r : lim;
-        const uint32_t c16 = dma_c16 ^ (uint32_t)(16 * (ii & (D == 128 ? 3 : 1)));
+        const uint32_t c16 = c16_of(ii);
         const int off = (wave * NIW + ii) * 1024;
         dma16(kb + (r * krs + c16), ks + off);
         dma16(vb + (r * vrs + c16), vs + off);
@@ -1059,11 +1075,13 @@ __global__ __launch_bounds__(kPPThreads, 1) void attn_fwd_pp_kernel(AttnParams p
 
 template <int D, typename E>
 int launch(const AttnParams& prm, int block_q, hipStream_t stream) {
-  if (block_q == kPPBM) {
-    hipLaunchKernelGGL((attn_fwd_pp_kernel<D, E>), dim3(prm.total_work), dim3(kPPThreads), 0, stream, prm);
-  } else {
-    hipLaunchKernelGGL((attn_fwd_kernel<D, E>), dim3(prm.total_work), dim3(kThreads), 0, stream, prm);
+  if constexpr (D != 256) {
+    if (block_q == kPPBM) {
+      hipLaunchKernelGGL((attn_fwd_pp_kernel<D, E>), dim3(prm.total_work), dim3(kPPThreads), 0, stream, prm);
+      return launch_status("lvsa_attn_fwd");
+    }
   }
+  hipLaunchKernelGGL((attn_fwd_kernel<D, E>), dim3(prm.total_work), dim3(kThreads), 0, stream, prm);
   return launch_status("lvsa_attn_fwd");
 }
 
@@ -1082,8 +1100,10 @@ using namespace lvsa;
 extern "C" int lvsa_attn_fwd(const lvsa_attn_args* a, hipStream_t stream) {
   clear_error();
   LVSA_REQUIRE(a != nullptr, LVSA_ERR_INVALID_ARG, "lvsa_attn_fwd: null args");
-  LVSA_REQUIRE(a->D == 64 || a->D == 128, LVSA_ERR_UNSUPPORTED, "lvsa_attn_fwd: head_dim %d not supported (64, 128)",
-               a->D);
+  LVSA_REQUIRE(a->D == 64 || a->D == 128 || a->D == 256, LVSA_ERR_UNSUPPORTED,
+               "lvsa_attn_fwd: head_dim %d not supported (64, 128, 256)", a->D);
+  LVSA_REQUIRE(a->D != 256 || a->block_q == kBM, LVSA_ERR_UNSUPPORTED,
+               "lvsa_attn_fwd: head_dim 256 runs 128-row tiles (block_q %d)", a->block_q);
   LVSA_REQUIRE(a->dtype == LVSA_BF16 || a->dtype == LVSA_FP16, LVSA_ERR_UNSUPPORTED, "lvsa_attn_fwd: dtype %d",
                a->dtype);
   LVSA_REQUIRE(a->B >= 1 && a->H >= 1 && a->Hkv >= 1 && a->H % a->Hkv == 0, LVSA_ERR_INVALID_ARG,
@@ -1165,6 +1185,8 @@ extern "C" int lvsa_attn_fwd(const lvsa_attn_args* a, hipStream_t stream) {
   p.k_tok0 = a->k_tok0;
   p.total_work = (int)work;
   const int bq = a->block_q;
+  if (a->D == 256)
+    return a->dtype == LVSA_BF16 ? launch<256, __bf16>(p, bq, stream) : launch<256, _Float16>(p, bq, stream);
   if (a->D == 128)
     return a->dtype == LVSA_BF16 ? launch<128, __bf16>(p, bq, stream) : launch<128, _Float16>(p, bq, stream);
   return a->dtype == LVSA_BF16 ? launch<64, __bf16>(p, bq, stream) : launch<64, _Float16>(p, bq, stream);

@@ -56,6 +56,10 @@ SMALL = [
     (5, 30, 10, 1, None, 0, 2, 2, 64, 0, torch.bfloat16),    # W > T: dense
     (1, 77, 0, 1, None, 0, 2, 2, 128, 3, torch.bfloat16),    # single frame
     (17, 129, 2, 2, 5, 4, 2, 2, 128, 129, torch.float16),    # odd sizes, text tail
+    (9, 200, 1, 1, 4, 1, 4, 2, 96, 37, torch.bfloat16),      # D=96 (zero-padded to 128), GQA, text
+    (9, 256, 1, 1, 4, 3, 2, 2, 192, 0, torch.bfloat16),      # D=192 (zero-padded to 256)
+    (9, 200, 1, 1, 4, 1, 4, 4, 256, 37, torch.bfloat16),     # D=256, text
+    (13, 150, 1, 1, 4, 0, 3, 3, 256, 26, torch.float16),     # D=256, fp16, text
 ]
 
 
@@ -224,8 +228,8 @@ def test_batch_views_and_fp32_inputs(gpu):
 
 def test_rejects_unsupported_head_dim(gpu):
     m = _meta(4, 16, 1, 1, 2)
-    q = torch.randn(1, 64, 2, 96, device=gpu, dtype=torch.bfloat16)
-    with pytest.raises(ValueError, match="head_dim 96"):
+    q = torch.randn(1, 64, 2, 80, device=gpu, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="head_dim 80"):
         lv.lvsa_attention(q, q, q, m)
 
 
