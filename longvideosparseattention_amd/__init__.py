@@ -29,6 +29,8 @@ def __getattr__(name):
         from . import block_sparse as m
     elif name == "build_global_kv":
         from . import global_kv as m
+    elif name == "DistributedLVSAProcessor":
+        from . import processor as m
     else:
         raise AttributeError(f"module 'longvideosparseattention_amd' has no attribute {name!r}")
     value = getattr(m, name)
@@ -36,4 +38,4 @@ def __getattr__(name):
     return value
 
 
-__all__ = list(_SPARSE) + list(_BLOCK) + ["build_global_kv"]
+__all__ = list(_SPARSE) + list(_BLOCK) + ["build_global_kv", "DistributedLVSAProcessor"]
