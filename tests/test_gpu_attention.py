@@ -226,6 +226,52 @@ def test_batch_views_and_fp32_inputs(gpu):
     _close(out32, out.float(), "fp32 inputs", max_abs=1e-6, mean_abs=1e-7)
 
 
+EXTREME = ["hot", "cold", "cold_then_hot", "hot_then_cold"]
+
+
+@pytest.mark.parametrize("block_q", [128, 256], ids=["tile128", "tile256"])
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+@pytest.mark.parametrize("D", [64, 128, 256])
+@pytest.mark.parametrize("pattern", EXTREME)
+def test_extreme_logits(pattern, D, dt, block_q, gpu, monkeypatch):
+    """Logits far from N(0,1), where the exponent offset of a row has to move.
+
+    * hot: |s * scale| up to hundreds, so 2^(s * scale * log2 e) overflows fp32 without an offset.
+    * cold: every logit very negative, so the exponentials underflow without an offset.
+    * cold_then_hot / hot_then_cold: the key frames switch between the two, so a row's offset
+      first settles low and must move up, or must stay while later blocks vanish.
+    """
+    monkeypatch.setenv("LVSA_ATTN_BLOCK_Q", str(block_q))
+    T, P, W, n, kfi, off, H = 9, 96, 1, 1, 4, 1, 2
+    N = T * P
+    amp = 12.0 if dt == torch.bfloat16 else 5.0
+    g = torch.Generator().manual_seed(7)
+    q = torch.randn(1, N, H, D, generator=g)
+    k = torch.randn(1, N, H, D, generator=g)
+    v = torch.randn(1, N, H, D, generator=g)
+    hot_q, hot_k = amp * q, amp * k
+    cold_q, cold_k = amp * (q.abs() + 0.5), -amp * (k.abs() + 0.5)
+    key_frame = torch.arange(N) // P
+    if pattern == "hot":
+        q, k = hot_q, hot_k
+    elif pattern == "cold":
+        q, k = cold_q, cold_k
+    else:
+        first_cold = pattern == "cold_then_hot"
+        early = (key_frame < T // 2).view(1, N, 1, 1)
+        q = cold_q if first_cold else hot_q.abs() + 0.5
+        k_cold, k_hot = cold_k, amp * (k.abs() + 0.5)
+        k = torch.where(early, k_cold, k_hot) if first_cold else torch.where(early, k_hot, k_cold)
+    q, k, v = q.to(dt), k.to(dt), v.to(dt)
+    m = _meta(T, P, W, n, kfi, off)
+    o, lse = lv.lvsa_attention(q.to(gpu), k.to(gpu), v.to(gpu), m, return_lse=True)
+    rows = [set(r) for r in om.build_frame_mask(T, P, W, n, kfi, offset=off).rows]
+    ro, rl = oa.per_frame_sdpa(q.float(), k.float(), v.float(), rows, P)
+    assert torch.isfinite(o.float()).all() and torch.isfinite(lse).all()
+    _close(o, ro, f"{pattern} D={D}")
+    torch.testing.assert_close(lse.cpu(), rl, atol=2e-2, rtol=1e-5)
+
+
 def test_rejects_unsupported_head_dim(gpu):
     m = _meta(4, 16, 1, 1, 2)
     q = torch.randn(1, 64, 2, 80, device=gpu, dtype=torch.bfloat16)
