@@ -79,6 +79,7 @@ class DistributedLVSAProcessor:
         self._use_flashinfer = False
         self._geometry_warned = False
         self._dense_plans = {}
+        self._pattern_cache = {}
         # Boundary guards stay fixed across rotations (lvsa_processor.py:135-140).
         self._boundary_guards = compute_boundary_guard_frames(
             total_num_latent_frames, total_num_latent_frames * num_patches // world,
@@ -92,6 +93,19 @@ class DistributedLVSAProcessor:
     # ── pattern state ──────────────────────────────────────────────────────
 
     def _build(self, offset: int) -> LVSAMetadata:
+        """The pattern for ``offset`` under the current window / kfi / sparsity.
+
+        Patterns are kept per parameter set: a denoising run cycles through
+        ``kfi`` offsets, so every rotation after the first cycle reuses the
+        metadata together with its device mask and block plans."""
+        key = (offset, self.window_size, self.key_frame_interval, self._sparsity_scale)
+        meta = self._pattern_cache.get(key)
+        if meta is None:
+            meta = self._build_uncached(offset)
+            self._pattern_cache[key] = meta
+        return meta
+
+    def _build_uncached(self, offset: int) -> LVSAMetadata:
         return LVSAMetadata.build(
             total_latent_frames=self.total_num_frames, num_patches=self.num_patches,
             window_size=self.window_size, n_first_frames=self.n_first_frames,

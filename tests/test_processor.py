@@ -123,6 +123,23 @@ class TestDynamicReconfiguration:
         p.set_step(5)
         assert p._metadata is m
 
+    def test_rotation_cycle_reuses_patterns(self):
+        """A second cycle through the kfi offsets reuses the first cycle's metadata
+        (and with it the device mask and plans); each offset still matches the oracle."""
+        p = _proc(T=21, kfi=4)
+        first = {}
+        for step in range(4):
+            p.set_step(step)
+            first[step % 4] = p._metadata
+        assert len({id(m) for m in first.values()}) == 4
+        for step in range(4, 12):
+            p.set_step(step)
+            assert p._metadata is first[step % 4]
+            _assert_matches_oracle(p)
+        p.set_window_size(2)
+        assert all(p._metadata is not m for m in first.values())
+        _assert_matches_oracle(p)
+
     def test_no_kfi_is_noop(self):
         p = _proc(kfi=None)
         m = p._metadata
