@@ -1,1089 +1,10 @@
-// Block-sparse flash-attention forward for LVSA on gfx950 (MI355X).
-//
-// Work unit: one query tile of BM = 128 rows of one head (4 waves x 32 rows)
-// walks the key blocks (BN = 64 rows each) listed for it by the block plan.
-//
-//   S^T = K · Q^T      v_mfma_f32_32x32x16_{bf16,f16}: A = K rows from LDS
-//                      (ds_read_b128), B = Q held in registers for the tile
-//   softmax            every lane owns one query row (column of S^T): 16 of
-//                      the 32 keys of a 32-key sub-tile, the other 16 sit in
-//                      lane ^ 32; the running max uses a lazy rescale (O and
-//                      the row sum are rescaled only when the block maximum
-//                      exceeds the running one by more than 2^8)
-//   O^T += V^T · P^T   A = V^T read from the row-major LDS tile with
-//                      ds_read_b64_tr_b16, B = P (bf16/f16) straight from the
-//                      S^T accumulator registers (key order permuted
-//                      identically on both operands)
-//
-// K and V tiles are DMA'd global -> LDS (global_load_lds_dwordx4) into a
-// double buffer, with a 16-byte-chunk XOR swizzle that keeps both the K reads
-// and the transposing V reads free of bank conflicts.  The LDS image of a
-// tile is row-major, so K and V are read in place from the caller's
-// [B, S, H, D] tensors: no gather, no transpose, no padding copies.
-#include "lvsa_common.h"
+// Block-sparse flash-attention forward for LVSA on gfx950 (MI355X): the C ABI
+// entry point (lvsa_attn_fwd) and the D = 64 / 256 instantiations.  The
+// kernels are in lvsa_attn_kernels.h; D = 128 is launched from
+// lvsa_attn_d128.hip.
+#include "lvsa_attn_kernels.h"
 
-#include <type_traits>
-
-namespace lvsa {
 namespace {
-
-constexpr int kBM = 128;
-constexpr int kBN = 64;
-constexpr int kWaves = 4;
-constexpr int kThreads = 64 * kWaves;
-constexpr int kXcds = 8;
-
-typedef float floatx16 __attribute__((ext_vector_type(16)));
-typedef short shortx4 __attribute__((ext_vector_type(4)));
-typedef short shortx8 __attribute__((ext_vector_type(8)));
-typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) char lds_char;
-
-struct AttnParams {
-  const char* q;
-  const char* k;
-  const char* v;
-  const char* kx;
-  const char* vx;
-  const char* qt;
-  char* o;
-  char* ot;
-  float* lse;
-  float* lse_t;
-  int64_t q_str[3], k_str[3], v_str[3], kx_str[3], vx_str[3], qt_str[3], o_str[3], ot_str[3];
-  int B, H, Hkv, group;
-  int n_q, n_k, n_x, n_tq;
-  float scale_log2;
-  const int32_t* tile_indptr;
-  const uint2* entries;
-  int n_tiles, n_vt, n_tt;
-  const uint32_t* rel;
-  int words, R, C, q_frame0;
-  int64_t q_tok0, k_tok0;
-  int total_work;
-};
-
-template <typename E>
-struct Ops;
-
-template <>
-struct Ops<__bf16> {
-  typedef __bf16 v8 __attribute__((ext_vector_type(8)));
-  typedef __bf16 v2 __attribute__((ext_vector_type(2)));
-  __device__ static floatx16 mfma(v8 a, v8 b, floatx16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-  }
-  __device__ static v2 pack(float a, float b) { return v2{(__bf16)a, (__bf16)b}; }
-  __device__ static float dot2(v2 a, float acc) {
-    const v2 one = {(__bf16)1.0f, (__bf16)1.0f};
-    return __builtin_amdgcn_fdot2_f32_bf16(a, one, acc, false);
-  }
-  __device__ static unsigned short bits(float x) { return __builtin_bit_cast(unsigned short, (__bf16)x); }
-  __device__ static v8 scale(v8 x, float a) {
-    v8 r;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) r[i] = (__bf16)((float)x[i] * a);
-    return r;
-  }
-};
-
-template <>
-struct Ops<_Float16> {
-  typedef _Float16 v8 __attribute__((ext_vector_type(8)));
-  typedef _Float16 v2 __attribute__((ext_vector_type(2)));
-  __device__ static floatx16 mfma(v8 a, v8 b, floatx16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
-  }
-  __device__ static v2 pack(float a, float b) { return v2{(_Float16)a, (_Float16)b}; }
-  __device__ static float dot2(v2 a, float acc) {
-    const v2 one = {(_Float16)1.0f, (_Float16)1.0f};
-    return __builtin_amdgcn_fdot2(a, one, acc, false);
-  }
-  __device__ static unsigned short bits(float x) { return __builtin_bit_cast(unsigned short, (_Float16)x); }
-  __device__ static v8 scale(v8 x, float a) {
-    v8 r;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) r[i] = (_Float16)((float)x[i] * a);
-    return r;
-  }
-};
-
-// 16-byte-chunk swizzle of LDS row r (r & 15 is all that matters).
-//  D = 128 (16 chunks/row, a row spans all 64 banks): a bijection on r & 15 so
-//    the 16 rows of a K read hit 16 distinct chunks, and bits 2-3 = r & 3 so
-//    the 4 rows of a transposing V read land in 4 distinct 64-byte quarters.
-//  D = 64 (8 chunks/row, 2 rows per bank line): a bijection on (r >> 1) & 7
-//    with bit 2 = (r >> 1) & 1 so rows r and r + 2 of a V read differ.
-//  D = 256 (32 chunks/row, a row spans the banks twice): the D = 128 swizzle on
-//    the low 4 chunk bits, which keeps both patterns inside one 256-byte half.
-template <int D>
-__device__ __forceinline__ int swz(int r) {
-  if constexpr (D == 128 || D == 256) {
-    return ((r & 3) << 2) | ((r >> 2) & 3);
-  } else {
-    return (((r >> 1) & 1) << 2) | (((r >> 2) & 1) << 1) | ((r >> 3) & 1);
-  }
-}
-
-__device__ __forceinline__ void dma16(const void* g, lds_char* l) {
-  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)l, 16, 0, 0);
-}
-
-// The same copy issued as inline asm.  The compiler does not see the LDS
-// write, so it inserts no vmcnt wait before later LDS reads it cannot prove
-// disjoint (it cannot for the ring stages, and such a wait makes every copy
-// synchronous); the kernel orders the copies itself with explicit vmcnt
-// waits and barriers.  The addresses are made uniform so both land in SGPRs;
-// the s_nop covers the M0-write -> LDS-DMA hazard.  Nothing else in a kernel
-// that uses this may rely on M0.
-__device__ __forceinline__ void dma16_async(const char* g, uint32_t voff, const lds_char* l) {
-  // readfirstlane returns int: go through uint32_t so nothing sign-extends
-  const uint64_t b = (uint64_t)g;
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32));
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b);
-  const uint64_t sb = ((uint64_t)hi << 32) | (uint64_t)lo;
-  const uint32_t la = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)l);
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(sb), "s"(la) : "m0");
-#pragma clang diagnostic pop
-}
-
-// 16 bytes per lane, global -> LDS, through a buffer resource: lanes whose
-// soffset + voffset + 16 exceed the resource's num_records read zeros (per
-// dword) and write them to LDS, with no memory access.  Issued as asm for
-// the same reason as dma16_async.
-__device__ __forceinline__ void dma16_buf(u32x4 rsrc, uint32_t voff, uint32_t soff, const lds_char* l) {
-  const uint32_t la = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)l);
-  const uint32_t so = (uint32_t)__builtin_amdgcn_readfirstlane((int)soff);
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-  asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" : : "v"(voff), "s"(rsrc), "s"(so), "s"(la) : "m0");
-#pragma clang diagnostic pop
-}
-
-__device__ __forceinline__ void wait_vm0() {
-  // s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima).
-  __builtin_amdgcn_s_waitcnt(0x0F70);
-}
-
-template <int D, typename E>
-// Two work-groups per CU, except at D = 256 (its O and Q fragments alone take
-// 192 registers per lane): one work-group, registers up to 512.
-__global__ __launch_bounds__(kThreads, D == 256 ? 1 : 2) void attn_fwd_kernel(AttnParams p) {
-  using O = Ops<E>;
-  using v8 = typename O::v8;
-  using v2 = typename O::v2;
-  constexpr int RB = D * 2;               // bytes per K/V row
-  constexpr int NCH = RB / 16;            // 16-byte chunks per row
-  constexpr int TILE = kBN * RB;          // bytes of one K or V block
-  constexpr int STAGE = 2 * TILE;         // K block + V block
-  constexpr int NI = TILE / 1024;         // 1 KiB DMA instructions per block
-  constexpr int NIW = NI / kWaves;        // per wave
-  constexpr int ND = D / 16;              // MFMA k-steps of S
-  constexpr int NT = D / 32;              // 32-wide d tiles of O
-  constexpr int RPI = 1024 / RB;          // block rows per DMA instruction
-  static_assert(NI % kWaves == 0, "tile must split evenly over waves");
-
-  __shared__ __attribute__((aligned(1024))) char smem_raw[2 * STAGE];
-  lds_char* smem = (lds_char*)smem_raw;
-
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int h = lane >> 5;        // half of the wave
-  const int i32 = lane & 31;      // query row of this lane within the wave
-
-  // XCD-aware work order: consecutive work items stay on one XCD (shared L2).
-  int w;
-  {
-    const int b = blockIdx.x;
-    const int per = p.total_work / kXcds, rem = p.total_work % kXcds;
-    const int x = b % kXcds, idx = b / kXcds;
-    w = x * per + (x < rem ? x : rem) + idx;
-  }
-  const int tslot = w % p.n_tiles;
-  const int rest = w / p.n_tiles;
-  const int head = rest % p.H;
-  const int batch = rest / p.H;
-  const int tile = tslot < p.n_tt ? p.n_vt + tslot : tslot - p.n_tt;  // text tiles (longest) first
-  const bool text = tile >= p.n_vt;
-  const int hk = head / p.group;
-
-  const char* qbase;
-  char* obase;
-  int64_t qrs, ors;
-  int nrows;
-  int64_t r0;
-  float* lse;
-  if (!text) {
-    qbase = p.q + 2 * (batch * p.q_str[0] + head * p.q_str[2]);
-    obase = p.o + 2 * (batch * p.o_str[0] + head * p.o_str[2]);
-    qrs = 2 * p.q_str[1];
-    ors = 2 * p.o_str[1];
-    nrows = p.n_q;
-    r0 = (int64_t)tile * kBM;
-    lse = p.lse ? p.lse + ((int64_t)batch * p.H + head) * p.n_q : nullptr;
-  } else {
-    qbase = p.qt + 2 * (batch * p.qt_str[0] + head * p.qt_str[2]);
-    obase = p.ot + 2 * (batch * p.ot_str[0] + head * p.ot_str[2]);
-    qrs = 2 * p.qt_str[1];
-    ors = 2 * p.ot_str[1];
-    nrows = p.n_tq;
-    r0 = (int64_t)(tile - p.n_vt) * kBM;
-    lse = p.lse_t ? p.lse_t + ((int64_t)batch * p.H + head) * p.n_tq : nullptr;
-  }
-  const int e0 = p.tile_indptr[tile], e1 = p.tile_indptr[tile + 1];
-
-  // Key sources: 0 = frame-structured key/value, 1 = dense extra rows.
-  const char* kb0 = p.k + 2 * (batch * p.k_str[0] + hk * p.k_str[2]);
-  const char* vb0 = p.v + 2 * (batch * p.v_str[0] + hk * p.v_str[2]);
-  const char* kb1 = p.n_x ? p.kx + 2 * (batch * p.kx_str[0] + hk * p.kx_str[2]) : kb0;
-  const char* vb1 = p.n_x ? p.vx + 2 * (batch * p.vx_str[0] + hk * p.vx_str[2]) : vb0;
-  const uint32_t krs0 = (uint32_t)(2 * p.k_str[1]), vrs0 = (uint32_t)(2 * p.v_str[1]);
-  const uint32_t krs1 = (uint32_t)(2 * p.kx_str[1]), vrs1 = (uint32_t)(2 * p.vx_str[1]);
-
-  // DMA geometry: instruction ii of this wave fills LDS bytes
-  // [(wave*NIW + ii) KiB, +1 KiB), i.e. block rows RPI*(wave*NIW + ii) + lane/NCH,
-  // physical chunk lane%NCH.  Because wave*NIW is a multiple of 4 (D=128) or
-  // 2 (D=64), the swizzle of those rows is  dma_c ^ ii  with a per-lane dma_c.
-  // (D = 256: two rows per instruction, the swizzle of instruction ii's
-  // rows is formed per instruction.)
-  const uint32_t dma_lr = (uint32_t)(lane / NCH);
-  uint32_t dma_c16;
-  if constexpr (D == 128) {
-    dma_c16 = (uint32_t)(((lane & 15) ^ ((lane >> 4) << 2)) * 16);
-  } else if constexpr (D == 64) {
-    dma_c16 = (uint32_t)(((lane & 7) ^ ((((lane >> 4) & 1) << 2) | (((lane >> 5) & 1) << 1))) * 16);
-  } else {
-    dma_c16 = 0;
-  }
-  auto c16_of = [&](int ii) __attribute__((always_inline)) {
-    if constexpr (D == 256) {
-      const uint32_t row = (uint32_t)(RPI * (wave * NIW + ii)) + dma_lr;
-      return (uint32_t)(((lane % NCH) ^ swz<D>((int)(row & 15))) * 16);
-    } else {
-      return dma_c16 ^ (uint32_t)(16 * (ii & (D == 128 ? 3 : 1)));
-    }
-  };
-
-  // Plan entries of this tile, 64 at a time in a VGPR (lane i holds entry
-  // base + i); a uniform entry is read with v_readlane.  The next batch is
-  // prefetched one batch ahead so a batch switch never waits on memory.
-  uint32_t ec_x = 0, ec_y = 0, en_x = 0, en_y = 0;
-  int eb = e0;
-  if (e0 + lane < e1) {
-    const uint2 t = p.entries[e0 + lane];
-    ec_x = t.x;
-    ec_y = t.y;
-  }
-  if (e0 + 64 + lane < e1) {
-    const uint2 t = p.entries[e0 + 64 + lane];
-    en_x = t.x;
-    en_y = t.y;
-  }
-
-  auto issue = [&](uint32_t ex, lds_char* ks) {
-    const bool extra = (ex >> 31) != 0;
-    const int64_t nsrc = extra ? p.n_x : p.n_k;
-    int64_t k0 = (int64_t)(ex & 0x7fffffffu) * kBN;
-    if (k0 >= nsrc) k0 = 0;  // never produced by the plan; keeps every DMA in bounds
-    const uint32_t krs = extra ? krs1 : krs0, vrs = extra ? vrs1 : vrs0;
-    const char* kb = (extra ? kb1 : kb0) + k0 * krs;
-    const char* vb = (extra ? vb1 : vb0) + k0 * vrs;
-    lds_char* vs = ks + TILE;
-    if (k0 + kBN <= nsrc) {
-      const uint32_t lk = dma_lr * krs, lv = dma_lr * vrs;
-#pragma unroll
-      for (int ii = 0; ii < NIW; ++ii) {
-        const uint32_t row0 = (uint32_t)(RPI * (wave * NIW + ii));
-        const uint32_t c16 = c16_of(ii);
-        const int off = (wave * NIW + ii) * 1024;
-        dma16(kb + row0 * krs + (lk + c16), ks + off);
-        dma16(vb + row0 * vrs + (lv + c16), vs + off);
-      }
-    } else {
-      // last block of a source: rows past its end re-read the last row (masked later)
-      const uint32_t lim = (uint32_t)(nsrc - 1 - k0);
-#pragma unroll
-      for (int ii = 0; ii < NIW; ++ii) {
-        uint32_t r = (uint32_t)(RPI * (wave * NIW + ii)) + dma_lr;
-        r = r < lim ? r : lim;
-        const uint32_t c16 = c16_of(ii);
-        const int off = (wave * NIW + ii) * 1024;
-        dma16(kb + (r * krs + c16), ks + off);
-        dma16(vb + (r * vrs + c16), vs + off);
-      }
-    }
-  };
-
-  // Q fragments (B operand of S^T = K Q^T): row i32 of this wave, d = 16c + 8h .. +7.
-  v8 qf[ND];
-  const int64_t my_row = r0 + 32 * wave + i32;
-  {
-    const int64_t qr = my_row < nrows ? my_row : (int64_t)nrows - 1;
-    const char* qp = qbase + qr * qrs + 16 * h;
-#pragma unroll
-    for (int c = 0; c < ND; ++c) qf[c] = *reinterpret_cast<const v8*>(qp + 32 * c);
-  }
-
-  // LDS read offsets (relative to a stage).
-  const int sw_k = swz<D>(i32 & 15);
-  int koff[ND];
-#pragma unroll
-  for (int c = 0; c < ND; ++c) koff[c] = i32 * RB + ((((2 * c + h) ^ sw_k)) << 4);
-  const int g16 = lane & 15;
-  const int rowA = 4 * h + (g16 >> 2);            // + 16*s (+8 for the second read)
-  const int sw_a = swz<D>(rowA), sw_b = swz<D>(rowA + 8);
-  const int dgrp = (lane >> 4) & 1;
-  int voffA[NT], voffB[NT];
-#pragma unroll
-  for (int dt = 0; dt < NT; ++dt) {
-    const int chunk = 4 * dt + 2 * dgrp + ((lane & 3) >> 1);
-    const int inb = (lane & 1) * 8;
-    voffA[dt] = rowA * RB + ((chunk ^ sw_a) << 4) + inb;
-    voffB[dt] = (rowA + 8) * RB + ((chunk ^ sw_b) << 4) + inb;
-  }
-
-  floatx16 oacc[NT];
-#pragma unroll
-  for (int dt = 0; dt < NT; ++dt) oacc[dt] = floatx16{0};
-  float m_run = -1e30f;                  // running max of s*scale*log2(e)
-  float l4[4] = {0.f, 0.f, 0.f, 0.f};    // this lane's share of the row sum, 4 partials
-  const float cs = p.scale_log2;
-  const int my_tile_row = 32 * wave + i32;
-
-  // One block.  STG (0/1) is the LDS stage of this block, a compile-time
-  // constant so every LDS address is a register plus an immediate.
-  uint32_t nx = 0, ny = 0;   // entry of the next block (uniform)
-  auto body = [&](auto stg_c, int e) {
-    constexpr int STG = decltype(stg_c)::value;
-    const uint32_t cx = nx, cy = ny;
-    wait_vm0();          // this block has landed (the only DMA in flight)
-    __syncthreads();     // ... for every wave; the other stage is free again
-    if (e + 1 < e1) {
-      if (e + 1 - eb == 64) {
-        eb += 64;
-        ec_x = en_x;
-        ec_y = en_y;
-        en_x = en_y = 0;
-        if (eb + 64 + lane < e1) {
-          const uint2 t = p.entries[eb + 64 + lane];
-          en_x = t.x;
-          en_y = t.y;
-        }
-      }
-      nx = __builtin_amdgcn_readlane(ec_x, e + 1 - eb);
-      ny = __builtin_amdgcn_readlane(ec_y, e + 1 - eb);
-      issue(nx, smem + (1 - STG) * STAGE);
-    }
-    const lds_char* ks = smem + STG * STAGE;
-    const lds_char* vs = ks + TILE;
-
-    // S^T for keys [0, 32) and [32, 64) of the block.
-    floatx16 s0 = floatx16{0}, s1 = floatx16{0};
-#pragma unroll
-    for (int c = 0; c < ND; ++c) {
-      const v8 a0 = *reinterpret_cast<const __attribute__((address_space(3))) v8*>(ks + koff[c]);
-      const v8 a1 = *reinterpret_cast<const __attribute__((address_space(3))) v8*>(ks + koff[c] + 32 * RB);
-      s0 = O::mfma(a0, qf[c], s0);
-      s1 = O::mfma(a1, qf[c], s1);
-    }
-
-    // Masks.  Bit r of `keep` covers register r%16 of key half r/16, which
-    // holds key 8q + j + 4h of the block with q = r/4, j = r%4.
-    const uint32_t kind = cy & 3u;
-    if (kind != kKindNone) {
-      uint32_t keep;
-      if (kind == kKindTwoPart) {
-        const int bits = (cy >> 2) & 0xF;
-        const int kb = (int)((cy >> 8) & 0xFF) - 4 * h;
-        const int qs = (cy >> 16) & 0xFF;
-        const bool rb = my_tile_row >= qs;
-        const uint32_t lo_ok = (bits >> (rb ? 2 : 0)) & 1;
-        const uint32_t hi_ok = (bits >> (rb ? 3 : 1)) & 1;
-        int n_lo = 0;
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          const int c = kb - 8 * q;
-          n_lo += c < 0 ? 0 : (c > 4 ? 4 : c);
-        }
-        const uint32_t lo_mask = n_lo >= 32 ? 0xFFFFFFFFu : ((1u << n_lo) - 1u);
-        keep = (lo_ok ? lo_mask : 0u) | (hi_ok ? ~lo_mask : 0u);
-      } else {
-        const bool extra = (cx >> 31) != 0;
-        const int64_t k0 = (int64_t)(cx & 0x7fffffffu) * kBN;
-        const int64_t nsrc = extra ? p.n_x : p.n_k;
-        const int64_t qtok = p.q_tok0 + (my_row < nrows ? my_row : (int64_t)nrows - 1);
-        const int qf_row = (int)(qtok / p.R) - p.q_frame0;
-        const uint32_t* relrow = p.rel + (int64_t)qf_row * p.words;
-        keep = 0;
-        for (int r = 0; r < 32; ++r) {
-          const int64_t key = k0 + 8 * (r >> 2) + 4 * h + (r & 3);
-          if (key < nsrc) {
-            const int64_t kf = (p.k_tok0 + key) / p.C;
-            if ((kf >> 5) < p.words && ((relrow[kf >> 5] >> (kf & 31)) & 1u)) keep |= 1u << r;
-          }
-        }
-      }
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        s0[r] = ((keep >> r) & 1u) ? s0[r] : -INFINITY;
-        s1[r] = ((keep >> (r + 16)) & 1u) ? s1[r] : -INFINITY;
-      }
-    }
-
-    // Block row max as a tree (both key halves, then the partner lane).
-    float t8m[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) t8m[i] = fmaxf(fmaxf(s0[2 * i], s0[2 * i + 1]), fmaxf(s1[2 * i], s1[2 * i + 1]));
-    float mx = fmaxf(fmaxf(fmaxf(t8m[0], t8m[1]), fmaxf(t8m[2], t8m[3])),
-                     fmaxf(fmaxf(t8m[4], t8m[5]), fmaxf(t8m[6], t8m[7])));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float mxs = mx * cs;
-    if (__builtin_amdgcn_ballot_w64(mxs > m_run + 8.0f)) {
-      const float m_new = fmaxf(m_run, mxs);
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) l4[i] *= alpha;
-#pragma unroll
-      for (int dt = 0; dt < NT; ++dt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
-      m_run = m_new;
-    }
-
-    // P = 2^(s*cs - m), packed to the MFMA B operand of each 16-key step.
-    v8 pb[4];
-#pragma unroll
-    for (int st = 0; st < 4; ++st) {
-      const floatx16& src = (st < 2) ? s0 : s1;
-      const int base = 8 * (st & 1);
-      v2 pk[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float a = __builtin_amdgcn_exp2f(__builtin_fmaf(src[base + 2 * j], cs, -m_run));
-        const float b = __builtin_amdgcn_exp2f(__builtin_fmaf(src[base + 2 * j + 1], cs, -m_run));
-        pk[j] = O::pack(a, b);
-        l4[j] = O::dot2(pk[j], l4[j]);
-      }
-      pb[st] = v8{pk[0][0], pk[0][1], pk[1][0], pk[1][1], pk[2][0], pk[2][1], pk[3][0], pk[3][1]};
-    }
-
-    // O^T += V^T P^T.
-#pragma unroll
-    for (int st = 0; st < 4; ++st) {
-#pragma unroll
-      for (int dt = 0; dt < NT; ++dt) {
-        const shortx4 ta = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) shortx4*)(vs + voffA[dt] + 16 * st * RB));
-        const shortx4 tb = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) shortx4*)(vs + voffB[dt] + 16 * st * RB));
-        const shortx8 t8 = shortx8{ta[0], ta[1], ta[2], ta[3], tb[0], tb[1], tb[2], tb[3]};
-        oacc[dt] = O::mfma(__builtin_bit_cast(v8, t8), pb[st], oacc[dt]);
-      }
-    }
-  };
-
-  if (e0 < e1) {
-    nx = __builtin_amdgcn_readlane(ec_x, 0);
-    ny = __builtin_amdgcn_readlane(ec_y, 0);
-    issue(nx, smem);
-  }
-  for (int e = e0; e < e1; e += 2) {
-    body(std::integral_constant<int, 0>{}, e);
-    if (e + 1 < e1) body(std::integral_constant<int, 1>{}, e + 1);
-  }
-
-  // Epilogue: combine the row sum of both halves, normalise, store.
-  const float l_run = (l4[0] + l4[1]) + (l4[2] + l4[3]);
-  const float l_tot = l_run + __shfl_xor(l_run, 32);
-  if (my_row < nrows) {
-    const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
-    char* op = obase + my_row * ors;
-#pragma unroll
-    for (int dt = 0; dt < NT; ++dt) {
-#pragma unroll
-      for (int rq = 0; rq < 4; ++rq) {
-        const int d0 = 32 * dt + 8 * rq + 4 * h;
-        uint2 pk;
-        pk.x = (uint32_t)O::bits(oacc[dt][4 * rq] * inv) | ((uint32_t)O::bits(oacc[dt][4 * rq + 1] * inv) << 16);
-        pk.y = (uint32_t)O::bits(oacc[dt][4 * rq + 2] * inv) | ((uint32_t)O::bits(oacc[dt][4 * rq + 3] * inv) << 16);
-        *reinterpret_cast<uint2*>(op + 2 * d0) = pk;
-      }
-    }
-    if (lse && h == 0) {
-      lse[my_row] = l_tot > 0.f ? (m_run + __log2f(l_tot)) * 0.69314718055994530942f : -INFINITY;
-    }
-  }
-}
-
-// ───────────── ping-pong kernel: 8 waves, 256 query rows per tile ─────────────
-//
-// Waves w and w + 4 of a 512-thread workgroup run on the same SIMD.  Group 0
-// (waves 0-3) and group 1 (waves 4-7) hold 32 query rows per wave and walk
-// the same key blocks one phase apart, separated by workgroup barriers:
-//
-//   phase        0       1       2       3       4   ...
-//   group 0    M(0)    S(0)    M(1)    S(1)    M(2)
-//   group 1     -      M(0)    S(0)    M(1)    S(1)
-//
-// M(j): S^T of block j and O += P V of block j - 1 (MFMA fed from LDS);
-// S(j): mask, row max, exp and row sums of block j (VALU).  At every phase
-// each SIMD runs one wave's MFMAs under the other wave's softmax.  K/V blocks
-// rotate through a 4-stage LDS ring: block b is read from phase 2b (S^T,
-// group 0) to phase 2b + 3 (P V, group 1), and group 0 DMAs block j + 2 from
-// its MFMA phase 2j, about three phases before its first use.
-// The four K tiles sit at [0, 4 TILE) and the four V tiles above them, and
-// the phase loop is unrolled over 8 phases so every stage is a compile-time
-// constant: each LDS read is a VGPR plus an immediate.  M phases are
-// branch-free: the V tile of stage 3 starts zeroed and P starts at 0, so the
-// P V of block -1 in M(0) adds zero, and the S^T of block n computed in M(n)
-// is never used.
-
-constexpr int kPPWaves = 8;
-constexpr int kPPThreads = 64 * kPPWaves;
-constexpr int kPPBM = 32 * kPPWaves;
-constexpr int kPPStages = 4;
-
-// Workgroup barrier that nothing crosses: the memory clobber orders LDS and
-// global accesses, the scheduling barriers keep arithmetic (the exps of a
-// softmax phase) from drifting into the next phase.
-__device__ __forceinline__ void wg_barrier() {
-  __builtin_amdgcn_sched_barrier(0);
-  asm volatile("s_barrier" ::: "memory");
-  __builtin_amdgcn_sched_barrier(0);
-}
-
-// s_waitcnt vmcnt(N) with expcnt and lgkmcnt left at their maxima.
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  static_assert(N >= 0 && N < 16, "vmcnt immediate");
-  __builtin_amdgcn_s_waitcnt(0x0F70 | N);
-}
-
-// v_permlane32_swap on a copy of x: afterwards {a, b} hold x of lanes 0-31
-// and x of lanes 32-63 (one in each), so max(a, b) / a + b combine lanes l
-// and l ^ 32.  Written as asm with both registers in/out: the two-result
-// builtin of this toolchain loses its second result.  The s_nops cover the
-// VALU-write -> permlane-read hazard and the reads of its results.
-__device__ __forceinline__ void swap_halves(float& a, float& b) {
-  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
-}
-// IEEE maximum (v_maximum3_f32 when chained): unlike fmaxf it needs no
-// canonicalisation of MFMA results first.
-__device__ __forceinline__ float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
-__device__ __forceinline__ float max_halves(float x) {
-  float a = x, b = x;
-  swap_halves(a, b);
-  return vmax(a, b);
-}
-// Materialise x here: keeps the compiler from sinking the computation of a
-// phase's results across the barrier into the phase that consumes them.
-template <typename T>
-__device__ __forceinline__ void pin(T& x) {
-  asm volatile("" : "+v"(x));
-}
-__device__ __forceinline__ float sum_halves(float x) {
-  float a = x, b = x;
-  swap_halves(a, b);
-  return a + b;
-}
-
-template <int D, typename E>
-__global__ __launch_bounds__(kPPThreads, 1) void attn_fwd_pp_kernel(AttnParams p) {
-  using O = Ops<E>;
-  using v8 = typename O::v8;
-  using v2 = typename O::v2;
-  constexpr int RB = D * 2;               // bytes per K/V row
-  constexpr int NCH = RB / 16;            // 16-byte chunks per row
-  constexpr int TILE = kBN * RB;          // bytes of one K or V block
-  constexpr int NI = TILE / 1024;         // 1 KiB DMA instructions per block
-  constexpr int NIW = NI / 4;             // per group-1 wave
-  constexpr int ND = D / 16;              // MFMA k-steps of S
-  constexpr int NT = D / 32;              // 32-wide d tiles of O
-  constexpr int RPI = 1024 / RB;          // block rows per DMA instruction
-  static_assert(NI % 4 == 0, "tile must split evenly over the DMA waves");
-
-  __shared__ __attribute__((aligned(1024))) char smem_raw[2 * kPPStages * TILE];
-  lds_char* smem = (lds_char*)smem_raw;
-
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int grp = wave >> 2;      // 0: MFMA on even phases, 1: on odd phases
-  const int dw = wave & 3;        // DMA slot of a group-1 wave
-  const int h = lane >> 5;
-  const int i32 = lane & 31;
-
-  // XCD-aware work order: consecutive work items stay on one XCD (shared L2).
-  int w;
-  {
-    const int b = blockIdx.x;
-    const int per = p.total_work / kXcds, rem = p.total_work % kXcds;
-    const int x = b % kXcds, idx = b / kXcds;
-    w = x * per + (x < rem ? x : rem) + idx;
-  }
-  const int tslot = w % p.n_tiles;
-  const int rest = w / p.n_tiles;
-  const int head = rest % p.H;
-  const int batch = rest / p.H;
-  const int tile = tslot < p.n_tt ? p.n_vt + tslot : tslot - p.n_tt;  // text tiles (longest) first
-  const bool text = tile >= p.n_vt;
-  const int hk = head / p.group;
-
-  const char* qbase;
-  char* obase;
-  int64_t qrs, ors;
-  int nrows;
-  int64_t r0;
-  float* lse;
-  if (!text) {
-    qbase = p.q + 2 * (batch * p.q_str[0] + head * p.q_str[2]);
-    obase = p.o + 2 * (batch * p.o_str[0] + head * p.o_str[2]);
-    qrs = 2 * p.q_str[1];
-    ors = 2 * p.o_str[1];
-    nrows = p.n_q;
-    r0 = (int64_t)tile * kPPBM;
-    lse = p.lse ? p.lse + ((int64_t)batch * p.H + head) * p.n_q : nullptr;
-  } else {
-    qbase = p.qt + 2 * (batch * p.qt_str[0] + head * p.qt_str[2]);
-    obase = p.ot + 2 * (batch * p.ot_str[0] + head * p.ot_str[2]);
-    qrs = 2 * p.qt_str[1];
-    ors = 2 * p.ot_str[1];
-    nrows = p.n_tq;
-    r0 = (int64_t)(tile - p.n_vt) * kPPBM;
-    lse = p.lse_t ? p.lse_t + ((int64_t)batch * p.H + head) * p.n_tq : nullptr;
-  }
-  const int e0 = p.tile_indptr[tile], e1 = p.tile_indptr[tile + 1];
-  const int n = e1 - e0;
-
-  const char* kb0 = p.k + 2 * (batch * p.k_str[0] + hk * p.k_str[2]);
-  const char* vb0 = p.v + 2 * (batch * p.v_str[0] + hk * p.v_str[2]);
-  const char* kb1 = p.n_x ? p.kx + 2 * (batch * p.kx_str[0] + hk * p.kx_str[2]) : kb0;
-  const char* vb1 = p.n_x ? p.vx + 2 * (batch * p.vx_str[0] + hk * p.vx_str[2]) : vb0;
-  const uint32_t krs0 = (uint32_t)(2 * p.k_str[1]), vrs0 = (uint32_t)(2 * p.v_str[1]);
-  const uint32_t krs1 = (uint32_t)(2 * p.kx_str[1]), vrs1 = (uint32_t)(2 * p.vx_str[1]);
-
-  // DMA geometry of a group-0 wave: instruction ii fills LDS KiB 4*ii + dw
-  // of a tile, i.e. block rows (4*ii + dw)*RPI + lane/NCH at physical chunk
-  // lane%NCH.  The swizzle of those rows depends on row & 15 = (dw*RPI +
-  // lane/NCH) & 15 only, so a lane's byte offset within the block is the
-  // same for every instruction of the wave and the instruction adds the
-  // uniform 4*ii*RPI rows as the buffer soffset.
-  const uint32_t dma_row = (uint32_t)(dw * RPI + lane / NCH);  // row of instruction 0
-  const uint32_t dma_c16 = (uint32_t)(((lane % NCH) ^ swz<D>((int)(dma_row & 15))) * 16);
-
-  // Plan entries, 64 per VGPR batch (lane i holds entry eb + i) with the
-  // following batch prefetched; a uniform entry is read with v_readlane.
-  uint32_t ec_x = 0, ec_y = 0, en_x = 0, en_y = 0;
-  int eb = e0;
-  if (e0 + lane < e1) {
-    const uint2 t = p.entries[e0 + lane];
-    ec_x = t.x;
-    ec_y = t.y;
-  }
-  if (e0 + 64 + lane < e1) {
-    const uint2 t = p.entries[e0 + 64 + lane];
-    en_x = t.x;
-    en_y = t.y;
-  }
-  // entry e, eb <= e < eb + 128
-  auto entry = [&](int e, uint32_t& x, uint32_t& y) __attribute__((always_inline)) {
-    const int d = e - eb;
-    if (d < 64) {
-      x = __builtin_amdgcn_readlane(ec_x, d);
-      y = __builtin_amdgcn_readlane(ec_y, d);
-    } else {
-      x = __builtin_amdgcn_readlane(en_x, d - 64);
-      y = __builtin_amdgcn_readlane(en_y, d - 64);
-    }
-  };
-  // slide the batches once no entry below e is needed any more
-  auto advance = [&](int e) __attribute__((always_inline)) {
-    if (e - eb >= 64) {
-      eb += 64;
-      ec_x = en_x;
-      ec_y = en_y;
-      en_x = en_y = 0;
-      if (eb + 64 + lane < e1) {
-        const uint2 t = p.entries[eb + 64 + lane];
-        en_x = t.x;
-        en_y = t.y;
-      }
-    }
-  };
-
-  // DMA of one block as 2*NIW single instructions that the MFMA phase
-  // interleaves with its MFMAs: instruction 2*ii (+1) copies 1 KiB of K (V)
-  // through a buffer resource that starts at the block's first row and ends
-  // after its last row inside the source, so the rows of a source's short
-  // last block past its end land as zeros (they are masked by the plan).
-  const uint32_t dofk0 = __umul24(dma_row, krs0) + dma_c16;
-  const uint32_t dofv0 = __umul24(dma_row, vrs0) + dma_c16;
-  struct BlockSrc {
-    u32x4 kr, vr;          // buffer resources of the block's K and V rows
-    uint32_t krs, vrs;     // row strides (bytes)
-    uint32_t dk, dv;       // per-lane offsets
-  };
-  auto prep = [&](uint32_t ex) __attribute__((always_inline)) {
-    const bool extra = (ex >> 31) != 0;
-    const int64_t nsrc = extra ? p.n_x : p.n_k;
-    int64_t k0 = (int64_t)(ex & 0x7fffffffu) * kBN;
-    if (k0 >= nsrc) k0 = 0;  // never produced by the plan; keeps every DMA in bounds
-    BlockSrc src;
-    src.krs = extra ? krs1 : krs0;
-    src.vrs = extra ? vrs1 : vrs0;
-    const uint64_t kb = (uint64_t)((extra ? kb1 : kb0) + k0 * src.krs);
-    const uint64_t vb = (uint64_t)((extra ? vb1 : vb0) + k0 * src.vrs);
-    const int64_t rows = nsrc - k0 < kBN ? nsrc - k0 : kBN;
-    // resource words: base [47:0] (stride 0), num_records in bytes, raw 32-bit data format
-    src.kr = u32x4{(uint32_t)kb, (uint32_t)(kb >> 32) & 0xFFFFu, (uint32_t)(rows * src.krs), 0x00020000u};
-    src.vr = u32x4{(uint32_t)vb, (uint32_t)(vb >> 32) & 0xFFFFu, (uint32_t)(rows * src.vrs), 0x00020000u};
-    src.dk = extra ? __umul24(dma_row, krs1) + dma_c16 : dofk0;
-    src.dv = extra ? __umul24(dma_row, vrs1) + dma_c16 : dofv0;
-    return src;
-  };
-  auto dma_one = [&](const BlockSrc& src, int bst, int k) __attribute__((always_inline)) {
-    const int ii = k >> 1;
-    const uint32_t r = (uint32_t)(4 * ii * RPI);
-    if (k & 1) dma16_buf(src.vr, src.dv, r * src.vrs, smem + (kPPStages + bst) * TILE + (4 * ii + dw) * 1024);
-    else dma16_buf(src.kr, src.dk, r * src.krs, smem + bst * TILE + (4 * ii + dw) * 1024);
-  };
-
-  // Q fragments (B operand of S^T = K Q^T): row i32 of this wave, d = 16c + 8h .. +7.
-  v8 qf[ND];
-  const int64_t my_row = r0 + 32 * wave + i32;
-  {
-    const int64_t qr = my_row < nrows ? my_row : (int64_t)nrows - 1;
-    const char* qp = qbase + qr * qrs + 16 * h;
-#pragma unroll
-    for (int c = 0; c < ND; ++c) qf[c] = *reinterpret_cast<const v8*>(qp + 32 * c);
-    // Q lands here, once: re-defining the fragments through asm leaves no
-    // load the compiler would wait for inside the loop, where the hardware
-    // counter also counts the K/V copies in flight.
-    wait_vm<0>();
-#pragma unroll
-    for (int c = 0; c < ND; ++c) pin(qf[c]);
-  }
-
-  // LDS read offsets (relative to a stage).
-  const int sw_k = swz<D>(i32 & 15);
-  int koff[ND];
-#pragma unroll
-  for (int c = 0; c < ND; ++c) koff[c] = i32 * RB + ((((2 * c + h) ^ sw_k)) << 4);
-  const int g16 = lane & 15;
-  const int rowA = 4 * h + (g16 >> 2);            // + 16*s (+8 for the second read)
-  const int sw_a = swz<D>(rowA), sw_b = swz<D>(rowA + 8);
-  const int dgrp = (lane >> 4) & 1;
-  int voffA[NT], voffB[NT];
-#pragma unroll
-  for (int dt = 0; dt < NT; ++dt) {
-    const int chunk = 4 * dt + 2 * dgrp + ((lane & 3) >> 1);
-    const int inb = (lane & 1) * 8;
-    voffA[dt] = kPPStages * TILE + rowA * RB + ((chunk ^ sw_a) << 4) + inb;
-    voffB[dt] = kPPStages * TILE + (rowA + 8) * RB + ((chunk ^ sw_b) << 4) + inb;
-  }
-
-  floatx16 oacc[NT];
-#pragma unroll
-  for (int dt = 0; dt < NT; ++dt) oacc[dt] = floatx16{0};
-  floatx16 s0 = floatx16{0}, s1 = floatx16{0};
-  v8 pb[4];
-#pragma unroll
-  for (int st = 0; st < 4; ++st) pb[st] = v8{};
-  float m_run = -1e30f;                  // running max of s*scale*log2(e)
-  float l4[4] = {0.f, 0.f, 0.f, 0.f};    // this lane's share of the row sum, 4 partials
-  const float cs = p.scale_log2;
-  const int my_tile_row = 32 * wave + i32;
-
-  // M(j) with K of block j in stage STG and V of block j - 1 in stage STG - 1:
-  // S^T (2*ND MFMAs) then O^T += V^T P^T (4*NT MFMAs) as one stream whose LDS
-  // operands are read LA MFMAs ahead.
-  constexpr int LA = 4;
-  constexpr int NQK = 2 * ND, NM = NQK + 4 * NT;
-  auto mphase = [&](auto stg_c, auto&& after_mfma) __attribute__((always_inline)) {
-    constexpr int STG = decltype(stg_c)::value;
-    constexpr int VSTG = (STG + kPPStages - 1) & (kPPStages - 1);
-    v8 opa[NM];
-    s0 = floatx16{0};
-    s1 = floatx16{0};
-#pragma unroll
-    for (int i = -LA; i < NM; ++i) {
-      const int li = i + LA;
-      if (li < NM) {
-        if (li < NQK) {
-          opa[li] = *reinterpret_cast<const __attribute__((address_space(3))) v8*>(
-              smem + koff[li >> 1] + (li & 1) * 32 * RB + STG * TILE);
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        } else {
-          const int k = li - NQK, st = k / NT, dt = k % NT;
-          const shortx4 ta = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (__attribute__((address_space(3))) shortx4*)(smem + voffA[dt] + VSTG * TILE + 16 * st * RB));
-          const shortx4 tb = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (__attribute__((address_space(3))) shortx4*)(smem + voffB[dt] + VSTG * TILE + 16 * st * RB));
-          opa[li] = __builtin_bit_cast(v8, shortx8{ta[0], ta[1], ta[2], ta[3], tb[0], tb[1], tb[2], tb[3]});
-          __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-        }
-      }
-      if (i >= 0) {
-        if (i < NQK) {
-          if (i & 1) s1 = O::mfma(opa[i], qf[i >> 1], s1);
-          else s0 = O::mfma(opa[i], qf[i >> 1], s0);
-        } else {
-          const int k = i - NQK;
-          oacc[k % NT] = O::mfma(opa[i], pb[k / NT], oacc[k % NT]);
-        }
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        after_mfma(i);
-      }
-    }
-    pin(s0);
-    pin(s1);
-#pragma unroll
-    for (int dt = 0; dt < NT; ++dt) pin(oacc[dt]);
-  };
-
-  // S(j): masks, row max, lazy rescale, P = 2^(s*cs - m) packed for the
-  // next M phase, row sums.
-  auto sphase = [&](int j) __attribute__((always_inline)) {
-    advance(e0 + j);
-    uint32_t cx, cy;
-    entry(e0 + j, cx, cy);
-    // Bit r of `keep` covers register r%16 of key half r/16, which holds key
-    // 8q + jj + 4h of the block with q = r/4, jj = r%4.
-    const uint32_t kind = cy & 3u;
-    if (kind != kKindNone) {
-      uint32_t keep;
-      if (kind == kKindTwoPart) {
-        const int bits = (cy >> 2) & 0xF;
-        const int kb = (int)((cy >> 8) & 0xFF) - 4 * h;
-        const int qs = (cy >> 16) & 0xFF;
-        const bool rb = my_tile_row >= qs;
-        const uint32_t lo_ok = (bits >> (rb ? 2 : 0)) & 1;
-        const uint32_t hi_ok = (bits >> (rb ? 3 : 1)) & 1;
-        int n_lo = 0;
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          const int c = kb - 8 * q;
-          n_lo += c < 0 ? 0 : (c > 4 ? 4 : c);
-        }
-        const uint32_t lo_mask = n_lo >= 32 ? 0xFFFFFFFFu : ((1u << n_lo) - 1u);
-        keep = (lo_ok ? lo_mask : 0u) | (hi_ok ? ~lo_mask : 0u);
-      } else {
-        const bool extra = (cx >> 31) != 0;
-        const int64_t k0 = (int64_t)(cx & 0x7fffffffu) * kBN;
-        const int64_t nsrc = extra ? p.n_x : p.n_k;
-        const int64_t qtok = p.q_tok0 + (my_row < nrows ? my_row : (int64_t)nrows - 1);
-        const int qf_row = (int)(qtok / p.R) - p.q_frame0;
-        const uint32_t* relrow = p.rel + (int64_t)qf_row * p.words;
-        keep = 0;
-        for (int r = 0; r < 32; ++r) {
-          const int64_t key = k0 + 8 * (r >> 2) + 4 * h + (r & 3);
-          if (key < nsrc) {
-            const int64_t kf = (p.k_tok0 + key) / p.C;
-            if ((kf >> 5) < p.words && ((relrow[kf >> 5] >> (kf & 31)) & 1u)) keep |= 1u << r;
-          }
-        }
-      }
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        s0[r] = ((keep >> r) & 1u) ? s0[r] : -INFINITY;
-        s1[r] = ((keep >> (r + 16)) & 1u) ? s1[r] : -INFINITY;
-      }
-    }
-
-    // block row max: four independent chains of v_maximum3, then the partner lane
-    float mc[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      float m = vmax(s0[4 * c], s0[4 * c + 1]);
-      m = vmax(m, s0[4 * c + 2]);
-      m = vmax(m, s0[4 * c + 3]);
-      m = vmax(m, s1[4 * c]);
-      m = vmax(m, s1[4 * c + 1]);
-      m = vmax(m, s1[4 * c + 2]);
-      mc[c] = vmax(m, s1[4 * c + 3]);
-    }
-    const float mx = max_halves(vmax(vmax(mc[0], mc[1]), vmax(mc[2], mc[3])));
-    const float mxs = mx * cs;
-    if (__builtin_amdgcn_ballot_w64(mxs > m_run + 8.0f)) {
-      const float m_new = vmax(m_run, mxs);
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) l4[i] *= alpha;
-#pragma unroll
-      for (int dt = 0; dt < NT; ++dt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
-      m_run = m_new;
-    }
-
-#pragma unroll
-    for (int st = 0; st < 4; ++st) {
-      const floatx16& src = (st < 2) ? s0 : s1;
-      const int base = 8 * (st & 1);
-      v2 pk[4];
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        const float a = __builtin_amdgcn_exp2f(__builtin_fmaf(src[base + 2 * jj], cs, -m_run));
-        const float b = __builtin_amdgcn_exp2f(__builtin_fmaf(src[base + 2 * jj + 1], cs, -m_run));
-        pk[jj] = O::pack(a, b);
-        l4[jj] = O::dot2(pk[jj], l4[jj]);
-      }
-      pb[st] = v8{pk[0][0], pk[0][1], pk[1][0], pk[1][1], pk[2][0], pk[2][1], pk[3][0], pk[3][1]};
-    }
-#pragma unroll
-    for (int st = 0; st < 4; ++st) pin(pb[st]);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) pin(l4[i]);
-    pin(m_run);
-#pragma unroll
-    for (int dt = 0; dt < NT; ++dt) pin(oacc[dt]);
-  };
-
-  // V tile of stage 3 = 0: read by the P V of block -1 in M(0) (with P = 0).
-  {
-    constexpr int NZ = TILE / (16 * kPPThreads);
-#pragma unroll
-    for (int z = 0; z < NZ; ++z)
-      *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(
-          smem + (2 * kPPStages - 1) * TILE + (z * kPPThreads + (int)threadIdx.x) * 16) = u32x4{0, 0, 0, 0};
-  }
-  __syncthreads();
-
-  // Block b of the plan, or a stand-in past the end: row 0 of a key source,
-  // DMA'd into a stage that is never read again (keeps every MFMA phase the
-  // same instruction stream and the DMA count per phase constant).
-  const uint32_t stand_in = p.n_k > 0 ? 0u : 0x80000000u;
-  auto block_src = [&](int b) __attribute__((always_inline)) {
-    uint32_t x = stand_in, y;
-    if (b < n) entry(e0 + b, x, y);
-    return prep(x);
-  };
-
-  // Prologue: group 0 starts blocks 0 and 1; block 0 lands before phase 0.
-  if (grp == 0) {
-    const BlockSrc s0b = block_src(0);
-#pragma unroll
-    for (int k = 0; k < 2 * NIW; ++k) dma_one(s0b, 0, k);
-    const BlockSrc s1b = block_src(1);
-#pragma unroll
-    for (int k = 0; k < 2 * NIW; ++k) dma_one(s1b, 1, k);
-    wait_vm<2 * NIW>();
-  }
-  wg_barrier();
-
-  // Group 0 runs phases 0 .. 2n: M(j) on phase 2j, S(j) on phase 2j + 1;
-  // group 1 runs them one phase later.  Both pass 2n + 1 barriers.  Group 0
-  // owns the DMA and spreads it over its MFMA phases (one instruction after
-  // every fourth MFMA): M(j) copies block j + 2, whose stage last held block
-  // j - 2 (read for the last time by group 1's M(j - 1) on phase 2j - 1), and
-  // S(j) ends with block j + 1 landed for M(j + 1) (only block j + 2 may
-  // still be in flight).  Blocks are processed 4 at a time so the stage of
-  // every block is a compile-time constant.
-  using I0 = std::integral_constant<int, 0>;
-  using I1 = std::integral_constant<int, 1>;
-  using I2 = std::integral_constant<int, 2>;
-  using I3 = std::integral_constant<int, 3>;
-  static_assert(2 * NIW * 4 <= NM, "one DMA instruction per four MFMAs");
-  if (grp == 0) {
-    auto mdma = [&](auto stg_c, int b) __attribute__((always_inline)) {
-      constexpr int BST = (decltype(stg_c)::value + 2) & (kPPStages - 1);
-      const BlockSrc src = block_src(b);
-      mphase(stg_c, [&](int i) __attribute__((always_inline)) {
-        if ((i & 3) == 1 && (i >> 2) < 2 * NIW) {
-          dma_one(src, BST, i >> 2);
-          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-        }
-      });
-    };
-    for (int j0 = 0;; j0 += 4) {
-      mdma(I0{}, j0 + 2);
-      wg_barrier();
-      if (j0 >= n) break;
-      sphase(j0);
-      wait_vm<2 * NIW>();
-      wg_barrier();
-      mdma(I1{}, j0 + 3);
-      wg_barrier();
-      if (j0 + 1 >= n) break;
-      sphase(j0 + 1);
-      wait_vm<2 * NIW>();
-      wg_barrier();
-      mdma(I2{}, j0 + 4);
-      wg_barrier();
-      if (j0 + 2 >= n) break;
-      sphase(j0 + 2);
-      wait_vm<2 * NIW>();
-      wg_barrier();
-      mdma(I3{}, j0 + 5);
-      wg_barrier();
-      if (j0 + 3 >= n) break;
-      sphase(j0 + 3);
-      wait_vm<2 * NIW>();
-      wg_barrier();
-    }
-    wait_vm<0>();  // stand-in copies still in flight land before the workgroup ends
-  } else {
-    auto none = [](int) {};
-    wg_barrier();
-    for (int j0 = 0;; j0 += 4) {
-      mphase(I0{}, none);
-      if (j0 >= n) break;
-      wg_barrier();
-      sphase(j0);
-      wg_barrier();
-      mphase(I1{}, none);
-      if (j0 + 1 >= n) break;
-      wg_barrier();
-      sphase(j0 + 1);
-      wg_barrier();
-      mphase(I2{}, none);
-      if (j0 + 2 >= n) break;
-      wg_barrier();
-      sphase(j0 + 2);
-      wg_barrier();
-      mphase(I3{}, none);
-      if (j0 + 3 >= n) break;
-      wg_barrier();
-      sphase(j0 + 3);
-      wg_barrier();
-    }
-  }
-
-  // Epilogue: combine the row sum of both halves, normalise, store.
-  const float l_run = (l4[0] + l4[1]) + (l4[2] + l4[3]);
-  const float l_tot = sum_halves(l_run);
-  if (my_row < nrows) {
-    const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
-    char* op = obase + my_row * ors;
-#pragma unroll
-    for (int dt = 0; dt < NT; ++dt) {
-#pragma unroll
-      for (int rq = 0; rq < 4; ++rq) {
-        const int d0 = 32 * dt + 8 * rq + 4 * h;
-        uint2 pk;
-        pk.x = (uint32_t)O::bits(oacc[dt][4 * rq] * inv) | ((uint32_t)O::bits(oacc[dt][4 * rq + 1] * inv) << 16);
-        pk.y = (uint32_t)O::bits(oacc[dt][4 * rq + 2] * inv) | ((uint32_t)O::bits(oacc[dt][4 * rq + 3] * inv) << 16);
-        *reinterpret_cast<uint2*>(op + 2 * d0) = pk;
-      }
-    }
-    if (lse && h == 0) {
-      lse[my_row] = l_tot > 0.f ? (m_run + __log2f(l_tot)) * 0.69314718055994530942f : -INFINITY;
-    }
-  }
-}
-
-template <int D, typename E>
-int launch(const AttnParams& prm, int block_q, hipStream_t stream) {
-  if constexpr (D != 256) {
-    if (block_q == kPPBM) {
-      hipLaunchKernelGGL((attn_fwd_pp_kernel<D, E>), dim3(prm.total_work), dim3(kPPThreads), 0, stream, prm);
-      return launch_status("lvsa_attn_fwd");
-    }
-  }
-  hipLaunchKernelGGL((attn_fwd_kernel<D, E>), dim3(prm.total_work), dim3(kThreads), 0, stream, prm);
-  return launch_status("lvsa_attn_fwd");
-}
 
 bool aligned16(const void* ptr, const int64_t* str, int n) {
   if (((uintptr_t)ptr) % 16) return false;
@@ -1093,7 +14,6 @@ bool aligned16(const void* ptr, const int64_t* str, int n) {
 }
 
 }  // namespace
-}  // namespace lvsa
 
 using namespace lvsa;
 
@@ -1187,7 +107,6 @@ extern "C" int lvsa_attn_fwd(const lvsa_attn_args* a, hipStream_t stream) {
   const int bq = a->block_q;
   if (a->D == 256)
     return a->dtype == LVSA_BF16 ? launch<256, __bf16>(p, bq, stream) : launch<256, _Float16>(p, bq, stream);
-  if (a->D == 128)
-    return a->dtype == LVSA_BF16 ? launch<128, __bf16>(p, bq, stream) : launch<128, _Float16>(p, bq, stream);
+  if (a->D == 128) return launch_d128(p, bq, a->dtype == LVSA_BF16, stream);
   return a->dtype == LVSA_BF16 ? launch<64, __bf16>(p, bq, stream) : launch<64, _Float16>(p, bq, stream);
 }
