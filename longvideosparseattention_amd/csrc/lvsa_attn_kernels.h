@@ -807,8 +807,9 @@ __global__ __launch_bounds__(kPPThreads, 1) void attn_fwd_pp_kernel(AttnParams p
 
   // M(j) with K of block j in stage STG and V of block j - 1 in stage STG - 1:
   // S^T (2*ND MFMAs) then O^T += V^T P^T (4*NT MFMAs) as one stream whose LDS
-  // operands are read LA MFMAs ahead.
-  constexpr int LA = 4;
+  // operands are read LA MFMAs ahead (3 measured best for D = 128 under its
+  // scheduler, 4 for D = 64).
+  constexpr int LA = D == 128 ? 3 : 4;
   constexpr int NQK = 2 * ND, NM = NQK + 4 * NT;
   auto mphase = [&](auto stg_c, auto&& after_mfma) __attribute__((always_inline)) {
     constexpr int STG = decltype(stg_c)::value;
@@ -1000,7 +1001,7 @@ __global__ __launch_bounds__(kPPThreads, 1) void attn_fwd_pp_kernel(AttnParams p
       constexpr int BST = (decltype(stg_c)::value + 2) & (kPPStages - 1);
       const BlockSrc src = block_src(b);
       mphase(stg_c, [&](int i) __attribute__((always_inline)) {
-        if ((i & 3) == 1 && (i >> 2) < 2 * NIW) {
+        if ((i & 3) == 3 && (i >> 2) < 2 * NIW) {  // after the last MFMA of each group of four
           dma_one(src, BST, i >> 2);
           __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
         }
