@@ -4,9 +4,14 @@
 // scheduler, which schedules the D = 128 ping-pong loop about 2% faster and
 // the D = 64 one slower).
 //
-// Work unit: one query tile of BM = 128 rows of one head (4 waves x 32 rows)
-// walks the key blocks (BN = 64 rows each) listed for it by the block plan.
-//
+// Two kernels walk the key blocks (BN = 64 rows each) that the block plan
+// lists for a query tile of one head:
+//   attn_fwd_pp_kernel   256-row tiles, 8 waves x 32 rows in two groups that
+//                        alternate an MFMA phase with a softmax phase (D = 64
+//                        and 128; the default);
+//   attn_fwd_kernel      128-row tiles, 4 waves x 32 rows, one barrier per
+//                        block (D = 256, whose Q and O need 320 registers).
+// Both compute, per wave and key block:
 //   S^T = K · Q^T      v_mfma_f32_32x32x16_{bf16,f16}: A = K rows from LDS
 //                      (ds_read_b128), B = Q held in registers for the tile
 //   softmax            every lane owns one query row (column of S^T): 16 of
@@ -19,11 +24,13 @@
 //                      S^T accumulator registers (key order permuted
 //                      identically on both operands)
 //
-// K and V tiles are DMA'd global -> LDS (global_load_lds_dwordx4) into a
-// double buffer, with a 16-byte-chunk XOR swizzle that keeps both the K reads
-// and the transposing V reads free of bank conflicts.  The LDS image of a
-// tile is row-major, so K and V are read in place from the caller's
-// [B, S, H, D] tensors: no gather, no transpose, no padding copies.
+// K and V blocks are copied global -> LDS without a VGPR round trip (the
+// 4-wave kernel: global_load_lds_dwordx4 into a double buffer; the ping-pong
+// kernel: buffer_load_dwordx4 ... lds into a 4-stage ring), with a
+// 16-byte-chunk XOR swizzle that keeps both the K reads and the transposing V
+// reads free of bank conflicts.  The LDS image of a block is row-major, so K
+// and V are read in place from the caller's [B, S, H, D] tensors: no gather,
+// no transpose, no padding copies.
 #pragma once
 #include "lvsa_common.h"
 
