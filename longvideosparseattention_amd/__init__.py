@@ -31,6 +31,8 @@ def __getattr__(name):
         from . import global_kv as m
     elif name == "DistributedLVSAProcessor":
         from . import processor as m
+    elif name == "step_attention":
+        from . import step_op as m
     else:
         raise AttributeError(f"module 'longvideosparseattention_amd' has no attribute {name!r}")
     value = getattr(m, name)
@@ -38,4 +40,4 @@ def __getattr__(name):
     return value
 
 
-__all__ = list(_SPARSE) + list(_BLOCK) + ["build_global_kv", "DistributedLVSAProcessor"]
+__all__ = list(_SPARSE) + list(_BLOCK) + ["build_global_kv", "DistributedLVSAProcessor", "step_attention"]
