@@ -225,7 +225,10 @@ def main(argv=None) -> int:
         "tflops_token_exact": round(fx / wall / 1e12, 2),
         "gflop_per_call_block": round(fb / args.steps / 1e9, 1),
         "hbm_gbs_algorithmic": round(bytes_per_call / (ms * 1e-3) / 1e9, 1),
-        "mask_and_plan_build_ms": round(sum(build_ms) / len(build_ms), 3),
+        # per offset, warm (median over offsets after the first); the first
+        # build also pays the one-time library load and code-object upload
+        "mask_and_plan_build_ms": round(sorted(build_ms[1:] or build_ms)[len(build_ms[1:] or build_ms) // 2], 3),
+        "mask_and_plan_first_build_ms": round(build_ms[0], 3),
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": traffic,
                      "traffic_source": traffic_src, "kernel": kernel, "kernel_ms": round(ev_ms, 4)},
