@@ -106,7 +106,8 @@ def test_global_indices_known_answers():
     for off in range(4):
         covered |= set(om.compute_global_indices(21, 1, 4, off))
     assert covered == set(range(21))
-    # SURVEY worked examples: CPU config and Wan 4x step 5 (85 mod 84 = 1).
+    # Worked examples: the CPU config (T=9, kfi=4, offset 3), Wan 4x at step 5 (offset 5; 85 wraps
+    # to frame 1 modulo 84) and CogVideoX (T=13, kfi=4, offset 0).
     assert om.compute_global_indices(9, 1, 4, 3) == [0, 2, 3, 7]
     assert om.compute_global_indices(84, 1, 8, 5) == [0, 1, 5, 13, 21, 29, 37, 45, 53, 61, 69, 77]
     assert om.compute_global_indices(13, 1, 4, 0) == [0, 4, 8, 12]
@@ -128,7 +129,7 @@ def test_auto_kfi_known_answers():
 
 
 def test_cpu_config_frame_rows():
-    # frame 1 attends {0,1,2,3,4,5,7}, not the naive {0,1,2,3,7}.
+    # The expanded window: frame 1 attends {0,1,2,3,4,5,7}, not the clipped {0,1,2,3,7}.
     m = om.build_frame_mask(9, 256, 1, 1, 4, offset=3)
     assert m.rows[1] == [0, 1, 2, 3, 4, 5, 7]
     assert all(len(r) == 7 for r in m.rows)
@@ -249,7 +250,7 @@ def test_block_flops_against_token_mask():
     assert fx == 4 * 12 * 128 * int(tm.sum())
     blocks = tm.reshape(N // 64, 64, N // 64, 64).any(axis=(1, 3))
     assert fb == 4 * 12 * 128 * int(blocks.sum()) * 64 * 64
-    assert abs(fb / 1e9 - 25.4) < 0.1   # 25.4 GFLOP
+    assert abs(fb / 1e9 - 25.4) < 0.1   # 25.4 GFLOP of active 64x64 blocks at the CPU config
 
 
 def test_token_mask_semantics_small():
