@@ -31,6 +31,7 @@ SOURCES = {
     "lvsa_mask.hip": [],
     "lvsa_attn.hip": [],
     "lvsa_attn_d128.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"],
+    "lvsa_attn_d96.hip": [],
 }
 
 HIPCC_FLAGS = [

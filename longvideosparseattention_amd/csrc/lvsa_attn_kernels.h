@@ -1,14 +1,14 @@
 // Kernels of the block-sparse attention forward (gfx950), shared by the
 // translation units that instantiate them: lvsa_attn.hip (C ABI, D = 64 and
-// 256) and lvsa_attn_d128.hip (D = 128, built with the max-ILP machine
+// 256), lvsa_attn_d128.hip (D = 128, built with the max-ILP machine
 // scheduler, which schedules the D = 128 ping-pong loop about 2% faster and
-// the D = 64 one slower).
+// the D = 64 one slower) and lvsa_attn_d96.hip (D = 96).
 //
 // Two kernels walk the key blocks (BN = 64 rows each) that the block plan
 // lists for a query tile of one head:
 //   attn_fwd_pp_kernel   256-row tiles, 8 waves x 32 rows in two groups that
-//                        alternate an MFMA phase with a softmax phase (D = 64
-//                        and 128; the default);
+//                        alternate an MFMA phase with a softmax phase (D = 64,
+//                        96 and 128; the default);
 //   attn_fwd_kernel      128-row tiles, 4 waves x 32 rows, one barrier per
 //                        block (D = 256, whose Q and O need 320 registers).
 // Both compute, per wave and key block:
@@ -62,8 +62,10 @@ struct AttnParams {
   int total_work;
 };
 
-// D = 128 launches (bf16 / fp16), compiled in their own translation unit.
+// D = 128 and D = 96 launches (bf16 / fp16), each compiled in its own
+// translation unit.
 int launch_d128(const AttnParams& prm, int block_q, bool bf16, hipStream_t stream);
+int launch_d96(const AttnParams& prm, int block_q, bool bf16, hipStream_t stream);
 
 namespace {
 
@@ -126,7 +128,9 @@ struct Ops<_Float16> {
 };
 
 // 16-byte-chunk swizzle of LDS row r (r & 15 is all that matters).
-//  D = 128 (16 chunks/row, a row spans all 64 banks): a bijection on r & 15 so
+//  D = 128, and D = 96 laid out on the same 256-byte row pitch (chunks 12-15
+//    of a D = 96 row hold zeros and are never read)
+//    (16 chunks/row, a row spans all 64 banks): a bijection on r & 15 so
 //    the 16 rows of a K read hit 16 distinct chunks, and bits 2-3 = r & 3 so
 //    the 4 rows of a transposing V read land in 4 distinct 64-byte quarters.
 //  D = 64 (8 chunks/row, 2 rows per bank line): a bijection on (r >> 1) & 7
@@ -135,7 +139,7 @@ struct Ops<_Float16> {
 //    the low 4 chunk bits, which keeps both patterns inside one 256-byte half.
 template <int D>
 __device__ __forceinline__ int swz(int r) {
-  if constexpr (D == 128 || D == 256) {
+  if constexpr (D == 96 || D == 128 || D == 256) {
     return ((r & 3) << 2) | ((r >> 2) & 3);
   } else {
     return (((r >> 1) & 1) << 2) | (((r >> 2) & 1) << 1) | ((r >> 3) & 1);
@@ -611,8 +615,9 @@ __global__ __launch_bounds__(kPPThreads, 1) void attn_fwd_pp_kernel(AttnParams p
   using O = Ops<E>;
   using v8 = typename O::v8;
   using v2 = typename O::v2;
-  constexpr int RB = D * 2;               // bytes per K/V row
-  constexpr int NCH = RB / 16;            // 16-byte chunks per row
+  constexpr int RB = (D == 96 ? 128 : D) * 2;  // bytes per K/V row in LDS (D = 96: the D = 128 pitch)
+  constexpr int NCH = RB / 16;            // 16-byte chunks per LDS row
+  constexpr int NCV = D / 8;              // of which hold data
   constexpr int TILE = kBN * RB;          // bytes of one K or V block
   constexpr int NI = TILE / 1024;         // 1 KiB DMA instructions per block
   constexpr int NIW = NI / 4;             // per group-1 wave
@@ -688,6 +693,16 @@ __global__ __launch_bounds__(kPPThreads, 1) void attn_fwd_pp_kernel(AttnParams p
   // uniform 4*ii*RPI rows as the buffer soffset.
   const uint32_t dma_row = (uint32_t)(dw * RPI + lane / NCH);  // row of instruction 0
   const uint32_t dma_c16 = (uint32_t)(((lane % NCH) ^ swz<D>((int)(dma_row & 15))) * 16);
+  // D = 96: a lane whose chunk lies past the row's data reads from an offset
+  // beyond every buffer resource's range, so its copy writes zeros to LDS and
+  // touches no memory.  Row strides are below 16 MiB, so with the soffset of
+  // at most 60 rows the sum stays below 2^32.
+  auto lane_off = [&](uint32_t row_stride) __attribute__((always_inline)) {
+    if constexpr (NCV < NCH) {
+      if (dma_c16 >= (uint32_t)(16 * NCV)) return 0x7FFF0000u;
+    }
+    return __umul24(dma_row, row_stride) + dma_c16;
+  };
 
   // Plan entries, 64 per VGPR batch (lane i holds entry eb + i) with the
   // following batch prefetched; a uniform entry is read with v_readlane.
@@ -734,8 +749,8 @@ __global__ __launch_bounds__(kPPThreads, 1) void attn_fwd_pp_kernel(AttnParams p
   // through a buffer resource that starts at the block's first row and ends
   // after its last row inside the source, so the rows of a source's short
   // last block past its end land as zeros (they are masked by the plan).
-  const uint32_t dofk0 = __umul24(dma_row, krs0) + dma_c16;
-  const uint32_t dofv0 = __umul24(dma_row, vrs0) + dma_c16;
+  const uint32_t dofk0 = lane_off(krs0);
+  const uint32_t dofv0 = lane_off(vrs0);
   struct BlockSrc {
     u32x4 kr, vr;          // buffer resources of the block's K and V rows
     uint32_t krs, vrs;     // row strides (bytes)
@@ -755,8 +770,8 @@ __global__ __launch_bounds__(kPPThreads, 1) void attn_fwd_pp_kernel(AttnParams p
     // resource words: base [47:0] (stride 0), num_records in bytes, raw 32-bit data format
     src.kr = u32x4{(uint32_t)kb, (uint32_t)(kb >> 32) & 0xFFFFu, (uint32_t)(rows * src.krs), 0x00020000u};
     src.vr = u32x4{(uint32_t)vb, (uint32_t)(vb >> 32) & 0xFFFFu, (uint32_t)(rows * src.vrs), 0x00020000u};
-    src.dk = extra ? __umul24(dma_row, krs1) + dma_c16 : dofk0;
-    src.dv = extra ? __umul24(dma_row, vrs1) + dma_c16 : dofv0;
+    src.dk = extra ? lane_off(krs1) : dofk0;
+    src.dv = extra ? lane_off(vrs1) : dofv0;
     return src;
   };
   auto dma_one = [&](const BlockSrc& src, int bst, int k) __attribute__((always_inline)) {
@@ -1002,14 +1017,15 @@ __global__ __launch_bounds__(kPPThreads, 1) void attn_fwd_pp_kernel(AttnParams p
   using I1 = std::integral_constant<int, 1>;
   using I2 = std::integral_constant<int, 2>;
   using I3 = std::integral_constant<int, 3>;
-  static_assert(2 * NIW * 4 <= NM, "one DMA instruction per four MFMAs");
+  constexpr int CI = NM / (2 * NIW);      // MFMAs per copy instruction (4; 3 for D = 96)
+  static_assert(CI >= 1 && 2 * NIW * CI <= NM, "copies must fit the MFMA phase");
   if (grp == 0) {
     auto mdma = [&](auto stg_c, int b) __attribute__((always_inline)) {
       constexpr int BST = (decltype(stg_c)::value + 2) & (kPPStages - 1);
       const BlockSrc src = block_src(b);
       mphase(stg_c, [&](int i) __attribute__((always_inline)) {
-        if ((i & 3) == 3 && (i >> 2) < 2 * NIW) {  // after the last MFMA of each group of four
-          dma_one(src, BST, i >> 2);
+        if (i % CI == CI - 1 && i / CI < 2 * NIW) {  // after the last MFMA of each group of CI
+          dma_one(src, BST, i / CI);
           __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
         }
       });
@@ -1093,13 +1109,20 @@ __global__ __launch_bounds__(kPPThreads, 1) void attn_fwd_pp_kernel(AttnParams p
 
 template <int D, typename E>
 int launch(const AttnParams& prm, int block_q, hipStream_t stream) {
-  if constexpr (D != 256) {
+  if constexpr (D == 96) {
+    (void)block_q;
+    hipLaunchKernelGGL((attn_fwd_pp_kernel<D, E>), dim3(prm.total_work), dim3(kPPThreads), 0, stream, prm);
+    return launch_status("lvsa_attn_fwd");
+  }
+  if constexpr (D != 256 && D != 96) {
     if (block_q == kPPBM) {
       hipLaunchKernelGGL((attn_fwd_pp_kernel<D, E>), dim3(prm.total_work), dim3(kPPThreads), 0, stream, prm);
       return launch_status("lvsa_attn_fwd");
     }
   }
-  hipLaunchKernelGGL((attn_fwd_kernel<D, E>), dim3(prm.total_work), dim3(kThreads), 0, stream, prm);
+  if constexpr (D != 96) {
+    hipLaunchKernelGGL((attn_fwd_kernel<D, E>), dim3(prm.total_work), dim3(kThreads), 0, stream, prm);
+  }
   return launch_status("lvsa_attn_fwd");
 }
 

@@ -23,11 +23,11 @@ _DTYPES = {torch.bfloat16: capi.LVSA_BF16, torch.float16: capi.LVSA_FP16}
 # and 256 with zero-padded Q/K/V (the zero columns add nothing to Q K^T) and
 # the softmax scale of the true head size.
 SUPPORTED_HEAD_DIMS = (64, 96, 128, 192, 256)
-_KERNEL_HEAD_DIM = {64: 64, 96: 128, 128: 128, 192: 256, 256: 256}
+_KERNEL_HEAD_DIM = {64: 64, 96: 96, 128: 128, 192: 256, 256: 256}
 
 
 def kernel_head_dim(head_dim: int) -> int:
-    """Head size the kernel runs for ``head_dim`` (96 -> 128, 192 -> 256)."""
+    """Head size the kernel runs for ``head_dim`` (192 -> 256, zero-padded)."""
     if head_dim not in _KERNEL_HEAD_DIM:
         raise ValueError(f"head_dim {head_dim} not supported by the gfx950 kernel (supported: {SUPPORTED_HEAD_DIMS})")
     return _KERNEL_HEAD_DIM[head_dim]
@@ -36,13 +36,16 @@ def kernel_head_dim(head_dim: int) -> int:
 def attn_block_q(head_dim: int = 128) -> int:
     """Query rows per attention tile, i.e. which kernel a plan is built for.
 
-    256 for kernel head sizes 64 and 128: the 8-wave kernel whose two wave
-    groups alternate MFMA and softmax phases.  128 for 256: the 4-wave kernel
-    (the 8-wave kernel's registers hold no 256-wide Q and O).
-    ``LVSA_ATTN_BLOCK_Q`` (128 or 256) overrides the choice for 64 and 128."""
+    256 for kernel head sizes 64, 96 and 128: the 8-wave kernel whose two
+    wave groups alternate MFMA and softmax phases.  128 for 256: the 4-wave
+    kernel (the 8-wave kernel's registers hold no 256-wide Q and O).
+    ``LVSA_ATTN_BLOCK_Q`` (128 or 256) overrides the choice for 64 and 128;
+    96 runs on the 8-wave kernel only."""
     kd = kernel_head_dim(head_dim)
     if kd == 256:
         return 128
+    if kd == 96:
+        return 256
     env = os.environ.get("LVSA_ATTN_BLOCK_Q")
     if env:
         return int(env)

@@ -91,8 +91,11 @@ def test_plan_sizes():
 def test_attn_rejects_bad_args_without_launching():
     lib = _capi.lib()
     a = _capi.AttnArgs()
-    a.D, a.dtype, a.B, a.H, a.Hkv = 96, 0, 1, 2, 2
+    a.D, a.dtype, a.B, a.H, a.Hkv = 80, 0, 1, 2, 2
     assert lib.lvsa_attn_fwd(C.byref(a), None) == -2
-    assert b"head_dim 96" in lib.lvsa_last_error()
+    assert b"head_dim 80" in lib.lvsa_last_error()
+    a.D, a.block_q = 96, 128
+    assert lib.lvsa_attn_fwd(C.byref(a), None) == -2
+    assert b"head_dim 96 runs 256-row tiles" in lib.lvsa_last_error()
     a.D, a.H, a.Hkv = 128, 3, 2
     assert lib.lvsa_attn_fwd(C.byref(a), None) == -1
