@@ -175,12 +175,12 @@ typedef struct lvsa_attn_args {
   float* lse;               /* optional [B, H, n_q] natural-log LSE             */
   float* lse_t;             /* optional [B, H, n_tq]                            */
   int64_t q_str[3], k_str[3], v_str[3], kx_str[3], vx_str[3], qt_str[3], o_str[3], ot_str[3];
-  int32_t B, H, Hkv, D;      /* D = 64, 96, 128 or 256 (callers pad 192 with zeros) */
+  int32_t B, H, Hkv, D;      /* D = 64, 96, 128, 192 or 256                      */
   int32_t n_q, n_k, n_x, n_tq;
   float scale;              /* softmax scale (reference: 1/sqrt(D))             */
   int32_t dtype;            /* lvsa_dtype                                       */
   /* plan (built with block_q = 128 or 256 query rows and block_k = 64;
-   * D = 256 runs 128-row tiles only, D = 96 256-row tiles only) */
+   * D = 192 and 256 run 128-row tiles only, D = 96 256-row tiles only) */
   int32_t block_q;
   const int32_t* tile_indptr;
   const uint32_t* entries;

@@ -32,6 +32,7 @@ SOURCES = {
     "lvsa_attn.hip": [],
     "lvsa_attn_d128.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"],
     "lvsa_attn_d96.hip": [],
+    "lvsa_attn_d192.hip": [],
 }
 
 HIPCC_FLAGS = [

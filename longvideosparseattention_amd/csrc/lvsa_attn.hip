@@ -1,7 +1,7 @@
 // Block-sparse flash-attention forward for LVSA on gfx950 (MI355X): the C ABI
 // entry point (lvsa_attn_fwd) and the D = 64 / 256 instantiations.  The
-// kernels are in lvsa_attn_kernels.h; D = 128 and D = 96 are launched from
-// lvsa_attn_d128.hip and lvsa_attn_d96.hip.
+// kernels are in lvsa_attn_kernels.h; D = 128, 96 and 192 are launched from
+// lvsa_attn_d128.hip, lvsa_attn_d96.hip and lvsa_attn_d192.hip.
 #include "lvsa_attn_kernels.h"
 
 namespace {
@@ -20,10 +20,10 @@ using namespace lvsa;
 extern "C" int lvsa_attn_fwd(const lvsa_attn_args* a, hipStream_t stream) {
   clear_error();
   LVSA_REQUIRE(a != nullptr, LVSA_ERR_INVALID_ARG, "lvsa_attn_fwd: null args");
-  LVSA_REQUIRE(a->D == 64 || a->D == 96 || a->D == 128 || a->D == 256, LVSA_ERR_UNSUPPORTED,
-               "lvsa_attn_fwd: head_dim %d not supported (64, 96, 128, 256)", a->D);
-  LVSA_REQUIRE(a->D != 256 || a->block_q == kBM, LVSA_ERR_UNSUPPORTED,
-               "lvsa_attn_fwd: head_dim 256 runs 128-row tiles (block_q %d)", a->block_q);
+  LVSA_REQUIRE(a->D == 64 || a->D == 96 || a->D == 128 || a->D == 192 || a->D == 256, LVSA_ERR_UNSUPPORTED,
+               "lvsa_attn_fwd: head_dim %d not supported (64, 96, 128, 192, 256)", a->D);
+  LVSA_REQUIRE(a->D < 192 || a->block_q == kBM, LVSA_ERR_UNSUPPORTED,
+               "lvsa_attn_fwd: head_dim %d runs 128-row tiles (block_q %d)", a->D, a->block_q);
   LVSA_REQUIRE(a->D != 96 || a->block_q == kPPBM, LVSA_ERR_UNSUPPORTED,
                "lvsa_attn_fwd: head_dim 96 runs 256-row tiles (block_q %d)", a->block_q);
   LVSA_REQUIRE(a->dtype == LVSA_BF16 || a->dtype == LVSA_FP16, LVSA_ERR_UNSUPPORTED, "lvsa_attn_fwd: dtype %d",
@@ -111,5 +111,6 @@ extern "C" int lvsa_attn_fwd(const lvsa_attn_args* a, hipStream_t stream) {
     return a->dtype == LVSA_BF16 ? launch<256, __bf16>(p, bq, stream) : launch<256, _Float16>(p, bq, stream);
   if (a->D == 128) return launch_d128(p, bq, a->dtype == LVSA_BF16, stream);
   if (a->D == 96) return launch_d96(p, bq, a->dtype == LVSA_BF16, stream);
+  if (a->D == 192) return launch_d192(p, bq, a->dtype == LVSA_BF16, stream);
   return a->dtype == LVSA_BF16 ? launch<64, __bf16>(p, bq, stream) : launch<64, _Float16>(p, bq, stream);
 }

@@ -2,7 +2,8 @@
 // translation units that instantiate them: lvsa_attn.hip (C ABI, D = 64 and
 // 256), lvsa_attn_d128.hip (D = 128, built with the max-ILP machine
 // scheduler, which schedules the D = 128 ping-pong loop about 2% faster and
-// the D = 64 one slower) and lvsa_attn_d96.hip (D = 96).
+// the D = 64 one slower), lvsa_attn_d96.hip (D = 96) and lvsa_attn_d192.hip
+// (D = 192).
 //
 // Two kernels walk the key blocks (BN = 64 rows each) that the block plan
 // lists for a query tile of one head:
@@ -62,10 +63,11 @@ struct AttnParams {
   int total_work;
 };
 
-// D = 128 and D = 96 launches (bf16 / fp16), each compiled in its own
+// D = 128, 96 and 192 launches (bf16 / fp16), each compiled in its own
 // translation unit.
 int launch_d128(const AttnParams& prm, int block_q, bool bf16, hipStream_t stream);
 int launch_d96(const AttnParams& prm, int block_q, bool bf16, hipStream_t stream);
+int launch_d192(const AttnParams& prm, int block_q, bool bf16, hipStream_t stream);
 
 namespace {
 
@@ -135,11 +137,13 @@ struct Ops<_Float16> {
 //    the 4 rows of a transposing V read land in 4 distinct 64-byte quarters.
 //  D = 64 (8 chunks/row, 2 rows per bank line): a bijection on (r >> 1) & 7
 //    with bit 2 = (r >> 1) & 1 so rows r and r + 2 of a V read differ.
-//  D = 256 (32 chunks/row, a row spans the banks twice): the D = 128 swizzle on
-//    the low 4 chunk bits, which keeps both patterns inside one 256-byte half.
+//  D = 256, and D = 192 laid out on the same 512-byte row pitch (chunks 24-31
+//    of a D = 192 row are never read) (32 chunks/row, a row spans the banks
+//    twice): the D = 128 swizzle on the low 4 chunk bits, which keeps both
+//    patterns inside one 256-byte half.
 template <int D>
 __device__ __forceinline__ int swz(int r) {
-  if constexpr (D == 96 || D == 128 || D == 256) {
+  if constexpr (D == 96 || D == 128 || D == 192 || D == 256) {
     return ((r & 3) << 2) | ((r >> 2) & 3);
   } else {
     return (((r >> 1) & 1) << 2) | (((r >> 2) & 1) << 1) | ((r >> 3) & 1);
@@ -189,14 +193,16 @@ __device__ __forceinline__ void wait_vm0() {
 }
 
 template <int D, typename E>
-// Two work-groups per CU, except at D = 256 (its O and Q fragments alone take
-// 192 registers per lane): one work-group, registers up to 512.
-__global__ __launch_bounds__(kThreads, D == 256 ? 1 : 2) void attn_fwd_kernel(AttnParams p) {
+// Two work-groups per CU, except at D = 192 and 256 (their O and Q fragments
+// alone take up to 192 registers per lane, and a 128 KiB LDS ring leaves room
+// for one work-group): one work-group, registers up to 512.
+__global__ __launch_bounds__(kThreads, D >= 192 ? 1 : 2) void attn_fwd_kernel(AttnParams p) {
   using O = Ops<E>;
   using v8 = typename O::v8;
   using v2 = typename O::v2;
-  constexpr int RB = D * 2;               // bytes per K/V row
-  constexpr int NCH = RB / 16;            // 16-byte chunks per row
+  constexpr int RB = (D == 192 ? 256 : D) * 2;  // bytes per K/V row in LDS (D = 192: the D = 256 pitch)
+  constexpr int NCH = RB / 16;            // 16-byte chunks per LDS row
+  constexpr int NCV = D / 8;              // of which hold data
   constexpr int TILE = kBN * RB;          // bytes of one K or V block
   constexpr int STAGE = 2 * TILE;         // K block + V block
   constexpr int NI = TILE / 1024;         // 1 KiB DMA instructions per block
@@ -279,9 +285,13 @@ __global__ __launch_bounds__(kThreads, D == 256 ? 1 : 2) void attn_fwd_kernel(At
     dma_c16 = 0;
   }
   auto c16_of = [&](int ii) __attribute__((always_inline)) {
-    if constexpr (D == 256) {
+    if constexpr (D >= 192) {
       const uint32_t row = (uint32_t)(RPI * (wave * NIW + ii)) + dma_lr;
-      return (uint32_t)(((lane % NCH) ^ swz<D>((int)(row & 15))) * 16);
+      int c = (lane % NCH) ^ swz<D>((int)(row & 15));
+      // D = 192: a slot past the row's data is never read; it copies a data
+      // chunk of the same row, so every address stays inside the row
+      if constexpr (NCV < NCH) c = c >= NCV ? c - (NCH - NCV) : c;
+      return (uint32_t)(c * 16);
     } else {
       return dma_c16 ^ (uint32_t)(16 * (ii & (D == 128 ? 3 : 1)));
     }
@@ -1114,7 +1124,7 @@ int launch(const AttnParams& prm, int block_q, hipStream_t stream) {
     hipLaunchKernelGGL((attn_fwd_pp_kernel<D, E>), dim3(prm.total_work), dim3(kPPThreads), 0, stream, prm);
     return launch_status("lvsa_attn_fwd");
   }
-  if constexpr (D != 256 && D != 96) {
+  if constexpr (D == 64 || D == 128) {
     if (block_q == kPPBM) {
       hipLaunchKernelGGL((attn_fwd_pp_kernel<D, E>), dim3(prm.total_work), dim3(kPPThreads), 0, stream, prm);
       return launch_status("lvsa_attn_fwd");

@@ -19,30 +19,26 @@ from . import _capi as capi
 
 _DTYPES = {torch.bfloat16: capi.LVSA_BF16, torch.float16: capi.LVSA_FP16}
 # Head sizes of the reference plugin (LVSABackend.get_supported_head_sizes,
-# backend.py:52-53).  The kernels run 64, 128 and 256; 96 and 192 run as 128
-# and 256 with zero-padded Q/K/V (the zero columns add nothing to Q K^T) and
-# the softmax scale of the true head size.
+# backend.py:52-53), all run natively: 96 on the 128 LDS layout, 192 on the
+# 256 one.
 SUPPORTED_HEAD_DIMS = (64, 96, 128, 192, 256)
-_KERNEL_HEAD_DIM = {64: 64, 96: 96, 128: 128, 192: 256, 256: 256}
-
-
 def kernel_head_dim(head_dim: int) -> int:
-    """Head size the kernel runs for ``head_dim`` (192 -> 256, zero-padded)."""
-    if head_dim not in _KERNEL_HEAD_DIM:
+    """Head size the kernel runs for ``head_dim``: every supported size natively."""
+    if head_dim not in SUPPORTED_HEAD_DIMS:
         raise ValueError(f"head_dim {head_dim} not supported by the gfx950 kernel (supported: {SUPPORTED_HEAD_DIMS})")
-    return _KERNEL_HEAD_DIM[head_dim]
+    return head_dim
 
 
 def attn_block_q(head_dim: int = 128) -> int:
     """Query rows per attention tile, i.e. which kernel a plan is built for.
 
-    256 for kernel head sizes 64, 96 and 128: the 8-wave kernel whose two
-    wave groups alternate MFMA and softmax phases.  128 for 256: the 4-wave
-    kernel (the 8-wave kernel's registers hold no 256-wide Q and O).
+    256 for head sizes 64, 96 and 128: the 8-wave kernel whose two wave
+    groups alternate MFMA and softmax phases.  128 for 192 and 256: the
+    4-wave kernel (the 8-wave kernel's registers hold no Q and O that wide).
     ``LVSA_ATTN_BLOCK_Q`` (128 or 256) overrides the choice for 64 and 128;
     96 runs on the 8-wave kernel only."""
     kd = kernel_head_dim(head_dim)
-    if kd == 256:
+    if kd >= 192:
         return 128
     if kd == 96:
         return 256
@@ -239,24 +235,7 @@ def attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, plan: BlockPlan,
     v = _prep(v, "value", dtype)
     B, n_q, H, D = q.shape
     Hkv = k.shape[2]
-    KD = kernel_head_dim(D)
-    if KD != D:
-        # 96 / 192: zero-pad to the kernel's head size, keep the true softmax
-        # scale, return the first D output columns.
-        pad = lambda t: None if t is None else torch.nn.functional.pad(t, (0, KD - D))  # noqa: E731
-        if scale is None:
-            scale = 1.0 / math.sqrt(D)
-        o, ot, lse, lse_t = attn_fwd(pad(q), pad(k), pad(v), plan, kx=pad(kx), vx=pad(vx), qt=pad(qt),
-                                     scale=scale, return_lse=return_lse)
-        o = o[..., :D]
-        ot = None if ot is None else ot[..., :D]
-        if out is not None:
-            out.copy_(o)
-            o = out
-        if out_t is not None and ot is not None:
-            out_t.copy_(ot)
-            ot = out_t
-        return o, ot, lse, lse_t
+    kernel_head_dim(D)  # raises for an unsupported head size
     if k.shape[0] != B or k.shape[3] != D or v.shape != k.shape:
         raise ValueError(f"key/value shapes {tuple(k.shape)} / {tuple(v.shape)} do not match query {tuple(q.shape)}")
     if H % Hkv:

@@ -97,5 +97,8 @@ def test_attn_rejects_bad_args_without_launching():
     a.D, a.block_q = 96, 128
     assert lib.lvsa_attn_fwd(C.byref(a), None) == -2
     assert b"head_dim 96 runs 256-row tiles" in lib.lvsa_last_error()
+    a.D, a.block_q = 192, 256
+    assert lib.lvsa_attn_fwd(C.byref(a), None) == -2
+    assert b"head_dim 192 runs 128-row tiles" in lib.lvsa_last_error()
     a.D, a.H, a.Hkv = 128, 3, 2
     assert lib.lvsa_attn_fwd(C.byref(a), None) == -1

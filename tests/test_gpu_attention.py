@@ -58,7 +58,8 @@ SMALL = [
     (17, 129, 2, 2, 5, 4, 2, 2, 128, 129, torch.float16),    # odd sizes, text tail
     (9, 200, 1, 1, 4, 1, 4, 2, 96, 37, torch.bfloat16),      # D=96 (native, 256-row tiles), GQA, text
     (13, 150, 1, 1, 4, 0, 3, 3, 96, 26, torch.float16),      # D=96, fp16, text
-    (9, 256, 1, 1, 4, 3, 2, 2, 192, 0, torch.bfloat16),      # D=192 (zero-padded to 256)
+    (9, 256, 1, 1, 4, 3, 2, 2, 192, 0, torch.bfloat16),      # D=192 (native, 128-row tiles)
+    (13, 150, 1, 1, 4, 0, 4, 2, 192, 26, torch.float16),     # D=192, fp16, GQA, text
     (9, 200, 1, 1, 4, 1, 4, 4, 256, 37, torch.bfloat16),     # D=256, text
     (13, 150, 1, 1, 4, 0, 3, 3, 256, 26, torch.float16),     # D=256, fp16, text
 ]
@@ -232,7 +233,7 @@ EXTREME = ["hot", "cold", "cold_then_hot", "hot_then_cold"]
 
 @pytest.mark.parametrize("block_q", [128, 256], ids=["tile128", "tile256"])
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
-@pytest.mark.parametrize("D", [64, 96, 128, 256])
+@pytest.mark.parametrize("D", [64, 96, 128, 192, 256])
 @pytest.mark.parametrize("pattern", EXTREME)
 def test_extreme_logits(pattern, D, dt, block_q, gpu, monkeypatch):
     """Logits far from N(0,1), where the exponent offset of a row has to move.

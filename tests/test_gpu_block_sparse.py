@@ -39,7 +39,7 @@ def _csr(n_qblocks, n_kblocks, empty, g):
 
 
 @pytest.mark.parametrize("block_q", [128, 256])
-@pytest.mark.parametrize("D", [64, 96, 128, 256])
+@pytest.mark.parametrize("D", [64, 96, 128, 192, 256])
 def test_arbitrary_csr_with_empty_rows(D, block_q, gpu, monkeypatch):
     monkeypatch.setenv("LVSA_ATTN_BLOCK_Q", str(block_q))
     R, C, H, HKV = 96, 80, 4, 2

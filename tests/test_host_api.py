@@ -142,12 +142,12 @@ def test_lazy_exports():
 
 def test_head_sizes_of_the_plugin():
     """The reference plugin's head sizes (backend.py:52-53) all map onto a kernel:
-    96 runs natively on 256-row tiles, 192 zero-padded as 256; 256 runs
-    128-row tiles."""
+    every size runs natively; 96 on 256-row tiles, 192 and 256 on 128-row
+    tiles."""
     from longvideosparseattention_amd import hip_ops
 
     assert hip_ops.SUPPORTED_HEAD_DIMS == (64, 96, 128, 192, 256)
-    assert [hip_ops.kernel_head_dim(d) for d in (64, 96, 128, 192, 256)] == [64, 96, 128, 256, 256]
+    assert [hip_ops.kernel_head_dim(d) for d in (64, 96, 128, 192, 256)] == [64, 96, 128, 192, 256]
     assert hip_ops.attn_block_q(256) == 128 and hip_ops.attn_block_q(192) == 128
     assert hip_ops.attn_block_q(96) == 256
     with pytest.raises(ValueError, match="head_dim 80"):
