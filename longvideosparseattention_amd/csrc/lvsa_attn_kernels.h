@@ -934,45 +934,112 @@ __global__ __launch_bounds__(kPPThreads, 1) void attn_fwd_pp_kernel(AttnParams p
       }
     }
 
-    // block row max: four independent chains of v_maximum3, then the partner lane
-    float mc[4];
+    if constexpr (D == 64) {
+      // D = 64: the rescale test reads this block's row sum instead of its
+      // row max (3% faster at D = 64; at D = 128 it disturbs the register
+      // allocation and runs slower).  P = 2^(s*cs - m) is formed against the
+      // running max of the earlier blocks, this lane's share summed in ls.
+      // The running max has to move only if some P exceeds 2^8, and then ls
+      // exceeds 2^8 too: the rare path (and the first block, whose running
+      // max is -1e30) takes the block's true row max and recomputes P.
+      float ls = 0.f;
+      {
+        const float nm = -m_run;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      float m = vmax(s0[4 * c], s0[4 * c + 1]);
-      m = vmax(m, s0[4 * c + 2]);
-      m = vmax(m, s0[4 * c + 3]);
-      m = vmax(m, s1[4 * c]);
-      m = vmax(m, s1[4 * c + 1]);
-      m = vmax(m, s1[4 * c + 2]);
-      mc[c] = vmax(m, s1[4 * c + 3]);
-    }
-    const float mx = max_halves(vmax(vmax(mc[0], mc[1]), vmax(mc[2], mc[3])));
-    const float mxs = mx * cs;
-    if (__builtin_amdgcn_ballot_w64(mxs > m_run + 8.0f)) {
-      const float m_new = vmax(m_run, mxs);
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+        for (int st = 0; st < 4; ++st) {
+          const floatx16& src = (st < 2) ? s0 : s1;
+          const int base = 8 * (st & 1);
+          v2 pk[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) l4[i] *= alpha;
+          for (int jj = 0; jj < 4; ++jj) {
+            const float a = __builtin_amdgcn_exp2f(__builtin_fmaf(src[base + 2 * jj], cs, nm));
+            const float b = __builtin_amdgcn_exp2f(__builtin_fmaf(src[base + 2 * jj + 1], cs, nm));
+            pk[jj] = O::pack(a, b);
+            ls = O::dot2(pk[jj], ls);
+          }
+          pb[st] = v8{pk[0][0], pk[0][1], pk[1][0], pk[1][1], pk[2][0], pk[2][1], pk[3][0], pk[3][1]};
+        }
+      }
+      if (__builtin_expect(__builtin_amdgcn_ballot_w64(!(ls <= 256.0f)) != 0, 0)) {
+        float mc[4];
 #pragma unroll
-      for (int dt = 0; dt < NT; ++dt)
+        for (int c = 0; c < 4; ++c) {
+          float m = vmax(s0[4 * c], s0[4 * c + 1]);
+          m = vmax(m, s0[4 * c + 2]);
+          m = vmax(m, s0[4 * c + 3]);
+          m = vmax(m, s1[4 * c]);
+          m = vmax(m, s1[4 * c + 1]);
+          m = vmax(m, s1[4 * c + 2]);
+          mc[c] = vmax(m, s1[4 * c + 3]);
+        }
+        const float mx = max_halves(vmax(vmax(mc[0], mc[1]), vmax(mc[2], mc[3])));
+        const float m_new = vmax(m_run, mx * cs);
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
-      m_run = m_new;
-    }
+        for (int i = 0; i < 4; ++i) l4[i] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < NT; ++dt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
+        m_run = m_new;
+        ls = 0.f;
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+          const floatx16& src = (st < 2) ? s0 : s1;
+          const int base = 8 * (st & 1);
+          v2 pk[4];
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+            const float a = __builtin_amdgcn_exp2f(__builtin_fmaf(src[base + 2 * jj], cs, -m_run));
+            const float b = __builtin_amdgcn_exp2f(__builtin_fmaf(src[base + 2 * jj + 1], cs, -m_run));
+            pk[jj] = O::pack(a, b);
+            ls = O::dot2(pk[jj], ls);
+          }
+          pb[st] = v8{pk[0][0], pk[0][1], pk[1][0], pk[1][1], pk[2][0], pk[2][1], pk[3][0], pk[3][1]};
+        }
+      }
+      l4[0] += ls;
+    } else {
+      // block row max: four independent chains of v_maximum3, then the partner lane
+      float mc[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        float m = vmax(s0[4 * c], s0[4 * c + 1]);
+        m = vmax(m, s0[4 * c + 2]);
+        m = vmax(m, s0[4 * c + 3]);
+        m = vmax(m, s1[4 * c]);
+        m = vmax(m, s1[4 * c + 1]);
+        m = vmax(m, s1[4 * c + 2]);
+        mc[c] = vmax(m, s1[4 * c + 3]);
+      }
+      const float mx = max_halves(vmax(vmax(mc[0], mc[1]), vmax(mc[2], mc[3])));
+      const float mxs = mx * cs;
+      if (__builtin_amdgcn_ballot_w64(mxs > m_run + 8.0f)) {
+        const float m_new = vmax(m_run, mxs);
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) l4[i] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < NT; ++dt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
+        m_run = m_new;
+      }
 
 #pragma unroll
-    for (int st = 0; st < 4; ++st) {
-      const floatx16& src = (st < 2) ? s0 : s1;
-      const int base = 8 * (st & 1);
-      v2 pk[4];
+      for (int st = 0; st < 4; ++st) {
+        const floatx16& src = (st < 2) ? s0 : s1;
+        const int base = 8 * (st & 1);
+        v2 pk[4];
 #pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        const float a = __builtin_amdgcn_exp2f(__builtin_fmaf(src[base + 2 * jj], cs, -m_run));
-        const float b = __builtin_amdgcn_exp2f(__builtin_fmaf(src[base + 2 * jj + 1], cs, -m_run));
-        pk[jj] = O::pack(a, b);
-        l4[jj] = O::dot2(pk[jj], l4[jj]);
+        for (int jj = 0; jj < 4; ++jj) {
+          const float a = __builtin_amdgcn_exp2f(__builtin_fmaf(src[base + 2 * jj], cs, -m_run));
+          const float b = __builtin_amdgcn_exp2f(__builtin_fmaf(src[base + 2 * jj + 1], cs, -m_run));
+          pk[jj] = O::pack(a, b);
+          l4[jj] = O::dot2(pk[jj], l4[jj]);
+        }
+        pb[st] = v8{pk[0][0], pk[0][1], pk[1][0], pk[1][1], pk[2][0], pk[2][1], pk[3][0], pk[3][1]};
       }
-      pb[st] = v8{pk[0][0], pk[0][1], pk[1][0], pk[1][1], pk[2][0], pk[2][1], pk[3][0], pk[3][1]};
     }
 #pragma unroll
     for (int st = 0; st < 4; ++st) pin(pb[st]);
