@@ -463,41 +463,90 @@ __global__ __launch_bounds__(kThreads, D >= 192 ? 1 : 2) void attn_fwd_kernel(At
       }
     }
 
-    // Block row max as a tree (both key halves, then the partner lane).
-    float t8m[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) t8m[i] = fmaxf(fmaxf(s0[2 * i], s0[2 * i + 1]), fmaxf(s1[2 * i], s1[2 * i + 1]));
-    float mx = fmaxf(fmaxf(fmaxf(t8m[0], t8m[1]), fmaxf(t8m[2], t8m[3])),
-                     fmaxf(fmaxf(t8m[4], t8m[5]), fmaxf(t8m[6], t8m[7])));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float mxs = mx * cs;
-    if (__builtin_amdgcn_ballot_w64(mxs > m_run + 8.0f)) {
-      const float m_new = fmaxf(m_run, mxs);
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) l4[i] *= alpha;
-#pragma unroll
-      for (int dt = 0; dt < NT; ++dt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
-      m_run = m_new;
-    }
-
-    // P = 2^(s*cs - m), packed to the MFMA B operand of each 16-key step.
     v8 pb[4];
+    if constexpr (D >= 192) {
+      // D >= 192: one wave per SIMD issues both the MFMAs and the softmax, so
+      // every softmax instruction counts.  The lazy-rescale test reads the
+      // block's row sum instead of its row max: P = 2^(s*cs - m) is formed
+      // against the running max of the earlier blocks; the running max has
+      // to move only if some P exceeds 2^8, and then this lane's share of the
+      // row sum (ls) exceeds 2^8 too.  The rare path (and the first block,
+      // whose running max is -1e30) takes the true row max and recomputes P.
+      auto exps = [&](float nm, float& ls) __attribute__((always_inline)) {
+        ls = 0.f;
 #pragma unroll
-    for (int st = 0; st < 4; ++st) {
-      const floatx16& src = (st < 2) ? s0 : s1;
-      const int base = 8 * (st & 1);
-      v2 pk[4];
+        for (int st = 0; st < 4; ++st) {
+          const floatx16& src = (st < 2) ? s0 : s1;
+          const int base = 8 * (st & 1);
+          v2 pk[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float a = __builtin_amdgcn_exp2f(__builtin_fmaf(src[base + 2 * j], cs, -m_run));
-        const float b = __builtin_amdgcn_exp2f(__builtin_fmaf(src[base + 2 * j + 1], cs, -m_run));
-        pk[j] = O::pack(a, b);
-        l4[j] = O::dot2(pk[j], l4[j]);
+          for (int j = 0; j < 4; ++j) {
+            const float a = __builtin_amdgcn_exp2f(__builtin_fmaf(src[base + 2 * j], cs, nm));
+            const float b = __builtin_amdgcn_exp2f(__builtin_fmaf(src[base + 2 * j + 1], cs, nm));
+            pk[j] = O::pack(a, b);
+            ls = O::dot2(pk[j], ls);
+          }
+          pb[st] = v8{pk[0][0], pk[0][1], pk[1][0], pk[1][1], pk[2][0], pk[2][1], pk[3][0], pk[3][1]};
+        }
+      };
+      float ls;
+      exps(-m_run, ls);
+      if (__builtin_expect(__builtin_amdgcn_ballot_w64(!(ls <= 256.0f)) != 0, 0)) {
+        float t8m[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) t8m[i] = fmaxf(fmaxf(s0[2 * i], s0[2 * i + 1]), fmaxf(s1[2 * i], s1[2 * i + 1]));
+        float mx = fmaxf(fmaxf(fmaxf(t8m[0], t8m[1]), fmaxf(t8m[2], t8m[3])),
+                         fmaxf(fmaxf(t8m[4], t8m[5]), fmaxf(t8m[6], t8m[7])));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float m_new = fmaxf(m_run, mx * cs);
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) l4[i] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < NT; ++dt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
+        m_run = m_new;
+        exps(-m_run, ls);
       }
-      pb[st] = v8{pk[0][0], pk[0][1], pk[1][0], pk[1][1], pk[2][0], pk[2][1], pk[3][0], pk[3][1]};
+      l4[0] += ls;
+    } else {
+      // Block row max as a tree (both key halves, then the partner lane).
+      float t8m[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) t8m[i] = fmaxf(fmaxf(s0[2 * i], s0[2 * i + 1]), fmaxf(s1[2 * i], s1[2 * i + 1]));
+      float mx = fmaxf(fmaxf(fmaxf(t8m[0], t8m[1]), fmaxf(t8m[2], t8m[3])),
+                       fmaxf(fmaxf(t8m[4], t8m[5]), fmaxf(t8m[6], t8m[7])));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float mxs = mx * cs;
+      if (__builtin_amdgcn_ballot_w64(mxs > m_run + 8.0f)) {
+        const float m_new = fmaxf(m_run, mxs);
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) l4[i] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < NT; ++dt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
+        m_run = m_new;
+      }
+
+      // P = 2^(s*cs - m), packed to the MFMA B operand of each 16-key step.
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        const floatx16& src = (st < 2) ? s0 : s1;
+        const int base = 8 * (st & 1);
+        v2 pk[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float a = __builtin_amdgcn_exp2f(__builtin_fmaf(src[base + 2 * j], cs, -m_run));
+          const float b = __builtin_amdgcn_exp2f(__builtin_fmaf(src[base + 2 * j + 1], cs, -m_run));
+          pk[j] = O::pack(a, b);
+          l4[j] = O::dot2(pk[j], l4[j]);
+        }
+        pb[st] = v8{pk[0][0], pk[0][1], pk[1][0], pk[1][1], pk[2][0], pk[2][1], pk[3][0], pk[3][1]};
+      }
+
     }
 
     // O^T += V^T P^T.
