@@ -50,7 +50,7 @@ def _assert_same(a, b, what):
         assert torch.equal(a[key], b[key]), (what, key)
 
 
-@pytest.mark.parametrize("D,offset", [(128, 0), (128, 3), (64, 1), (96, 2)])
+@pytest.mark.parametrize("D,offset", [(128, 0), (128, 3), (64, 1), (96, 2), (192, 3), (256, 0)])
 def test_step_graph_replays_match_eager(D, offset):
     dev = torch.device("cuda", 0)
     meta = lv.LVSAMetadata.build(total_latent_frames=T, num_patches=P, window_size=W, n_first_frames=N_FIRST,
