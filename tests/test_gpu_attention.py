@@ -93,6 +93,54 @@ def test_fused_attention_small(cfg, block_q, gpu, monkeypatch):
     torch.testing.assert_close(lse.cpu(), rl, atol=2e-2, rtol=0)
 
 
+def _random_cfg(seed):
+    """A seeded random geometry: frame sizes on and off the 64-key blocks,
+    every head size, GQA, text tokens, both dtypes and both tile heights."""
+    g = torch.Generator().manual_seed(1000 + seed)
+    pick = lambda xs: xs[int(torch.randint(len(xs), (1,), generator=g))]  # noqa: E731
+    T = int(torch.randint(1, 17, (1,), generator=g))
+    P = int(torch.randint(1, 301, (1,), generator=g))
+    W = pick([0, 1, 1, 2, 2, 3, 4])
+    n = pick([1, 1, 2, 3])
+    kfi = pick([None, 1, 2, 3, 4, 5, 8])
+    off = int(torch.randint(0, 8, (1,), generator=g)) % (kfi or 1)
+    D = pick([64, 96, 128, 192, 256])
+    Hkv = pick([1, 2, 3])
+    H = Hkv * pick([1, 2])
+    n_txt = pick([0, 0, 1, 17, 64, 100])
+    dt = pick([torch.bfloat16, torch.float16])
+    block_q = pick([128, 256])
+    return T, P, W, n, kfi, off, H, Hkv, D, n_txt, dt, block_q
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_geometries(seed, gpu, monkeypatch):
+    """Seeded random geometries through ``lvsa_attention`` against the fp32
+    oracle (video rows, text rows and both LSEs)."""
+    T, P, W, n, kfi, off, H, Hkv, D, n_txt, dt, block_q = _random_cfg(seed)
+    monkeypatch.setenv("LVSA_ATTN_BLOCK_Q", str(block_q))
+    N = T * P
+    m = _meta(T, P, W, n, kfi, off)
+    q, k, v, qt, kt, vt = _draw([(1, N, H, D), (1, N, Hkv, D), (1, N, Hkv, D), (1, n_txt, H, D),
+                                 (1, n_txt, Hkv, D), (1, n_txt, Hkv, D)], seed=seed, dtype=dt)
+    rows = [set(r) for r in om.build_frame_mask(T, P, W, n, kfi, offset=off).rows]
+    args = dict(k_text=kt.to(gpu), v_text=vt.to(gpu), q_text=qt.to(gpu)) if n_txt else {}
+    res = lv.lvsa_attention(q.to(gpu), k.to(gpu), v.to(gpu), m, return_lse=True, **args)
+    ro, rl = oa.per_frame_sdpa(q.float(), k.float(), v.float(), rows, P,
+                               k_extra=kt.float() if n_txt else None, v_extra=vt.float() if n_txt else None)
+    what = f"seed {seed}: T={T} P={P} W={W} n={n} kfi={kfi} off={off} H={H}/{Hkv} D={D} txt={n_txt} {dt} bq={block_q}"
+    if n_txt:
+        o, ot, lse, lse_t = res
+        rto, rtl = oa.text_row_attention(qt.float(), k.float(), v.float(), kt.float(), vt.float())
+        _close(ot, rto, what + " text rows")
+        torch.testing.assert_close(lse_t.cpu(), rtl, atol=2e-2, rtol=0, msg=what)
+    else:
+        o, lse = res
+    assert o.dtype == dt and o.shape == q.shape
+    _close(o, ro, what)
+    torch.testing.assert_close(lse.cpu(), rl, atol=2e-2, rtol=0, msg=what)
+
+
 def test_repeat_call_is_bitwise_identical(gpu):
     T, P, H, D = 12, 300, 4, 128
     m = _meta(T, P, 2, 1, 4, 1)
