@@ -24,15 +24,19 @@ INCLUDE = ROOT / "include"
 LIB_DIR = PKG / "_lib"
 LIB = LIB_DIR / "liblvsa_amd.so"
 ARCH = os.environ.get("LVSA_OFFLOAD_ARCH", "gfx950")
-# Translation units and their extra flags.  The D = 128 attention kernels get
-# the max-ILP machine scheduler: measured about 2% faster on the D = 128
-# configurations and slower on D = 64, hence a translation unit of their own.
+# Translation units and their extra flags: one unit per attention head size,
+# each with the machine scheduler measured fastest for it.  max-ILP: about 2%
+# faster on the D = 128 configurations (slower on 64 and 96).  iterative-maxocc:
+# the 4-wave kernels, about 6% faster at D = 192 and 21% at D = 256.
+MAXOCC = ["-mllvm", "-amdgpu-sched-strategy=iterative-maxocc"]
 SOURCES = {
     "lvsa_mask.hip": [],
     "lvsa_attn.hip": [],
-    "lvsa_attn_d128.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"],
+    "lvsa_attn_d64.hip": [],
     "lvsa_attn_d96.hip": [],
-    "lvsa_attn_d192.hip": [],
+    "lvsa_attn_d128.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"],
+    "lvsa_attn_d192.hip": MAXOCC,
+    "lvsa_attn_d256.hip": MAXOCC,
 }
 
 HIPCC_FLAGS = [

@@ -1,7 +1,8 @@
 // Block-sparse flash-attention forward for LVSA on gfx950 (MI355X): the C ABI
-// entry point (lvsa_attn_fwd) and the D = 64 / 256 instantiations.  The
-// kernels are in lvsa_attn_kernels.h; D = 128, 96 and 192 are launched from
-// lvsa_attn_d128.hip, lvsa_attn_d96.hip and lvsa_attn_d192.hip.
+// entry point (lvsa_attn_fwd), its argument checks and the dispatch by head
+// size.  The kernels are in lvsa_attn_kernels.h, instantiated per head size
+// in lvsa_attn_d64.hip, lvsa_attn_d96.hip, lvsa_attn_d128.hip,
+// lvsa_attn_d192.hip and lvsa_attn_d256.hip.
 #include "lvsa_attn_kernels.h"
 
 namespace {
@@ -107,10 +108,9 @@ extern "C" int lvsa_attn_fwd(const lvsa_attn_args* a, hipStream_t stream) {
   p.k_tok0 = a->k_tok0;
   p.total_work = (int)work;
   const int bq = a->block_q;
-  if (a->D == 256)
-    return a->dtype == LVSA_BF16 ? launch<256, __bf16>(p, bq, stream) : launch<256, _Float16>(p, bq, stream);
+  if (a->D == 256) return launch_d256(p, bq, a->dtype == LVSA_BF16, stream);
   if (a->D == 128) return launch_d128(p, bq, a->dtype == LVSA_BF16, stream);
   if (a->D == 96) return launch_d96(p, bq, a->dtype == LVSA_BF16, stream);
   if (a->D == 192) return launch_d192(p, bq, a->dtype == LVSA_BF16, stream);
-  return a->dtype == LVSA_BF16 ? launch<64, __bf16>(p, bq, stream) : launch<64, _Float16>(p, bq, stream);
+  return launch_d64(p, bq, a->dtype == LVSA_BF16, stream);
 }

@@ -63,11 +63,15 @@ struct AttnParams {
   int total_work;
 };
 
-// D = 128, 96 and 192 launches (bf16 / fp16), each compiled in its own
-// translation unit.
-int launch_d128(const AttnParams& prm, int block_q, bool bf16, hipStream_t stream);
+// Launches per head size (bf16 / fp16), each compiled in its own translation
+// unit (lvsa_attn_d<D>.hip): the compiler's code for one head size then does
+// not depend on which others are instantiated beside it, and each unit takes
+// the machine scheduler measured best for it.
+int launch_d64(const AttnParams& prm, int block_q, bool bf16, hipStream_t stream);
 int launch_d96(const AttnParams& prm, int block_q, bool bf16, hipStream_t stream);
+int launch_d128(const AttnParams& prm, int block_q, bool bf16, hipStream_t stream);
 int launch_d192(const AttnParams& prm, int block_q, bool bf16, hipStream_t stream);
+int launch_d256(const AttnParams& prm, int block_q, bool bf16, hipStream_t stream);
 
 namespace {
 
