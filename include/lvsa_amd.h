@@ -185,9 +185,20 @@ typedef struct lvsa_attn_args {
   const int32_t* tile_indptr;
   const uint32_t* entries;
   int32_t n_tiles, n_video_tiles;
-  /* relation for generic (kind 2) blocks */
+  /* relation for generic (kind 2) blocks: row (q_tok0 + r)/R - q_frame0 of
+   * rel [rel_rows x words] serves query row r, so every query row must fall
+   * inside it (checked)                                                       */
   const uint32_t* rel; int32_t words, R, C, q_frame0;
   int64_t q_tok0, k_tok0;
+  int32_t rel_rows;
+  /* optional scratch (device memory, lvsa_attn_workspace_query bytes): with
+   * it, each text-query tile's key range is split into chunks that run as
+   * separate work-groups after the video tiles and are merged by a second
+   * launch (exact log-sum-exp merge, as flashinfer_runner.py:184-197), so the
+   * long text tiles fill the launch's last round instead of lengthening it.
+   * Null: text tiles run whole, first.                                        */
+  void* workspace;
+  int64_t workspace_bytes;
 } lvsa_attn_args;
 
 /* Replaces lvsa_sdpa's per-frame loop (lvsa/sparse_attention.py:643-706), the
@@ -195,6 +206,12 @@ typedef struct lvsa_attn_args {
  * (lvsa/lvsa_processor.py:832-913; flashinfer_runner.py:96-198) and the dense
  * encoder-query attention (lvsa/lvsa_processor.py:710-735) with one launch.   */
 LVSA_API int lvsa_attn_fwd(const lvsa_attn_args* a, hipStream_t stream);
+
+/* Bytes of scratch lvsa_attn_fwd uses for the text-tile split of `a`
+ * (0 when there are no text queries); host only, nothing is launched.
+ * Replaces the float workspace the FlashInfer wrapper is planned with
+ * (flashinfer_runner.py:75-79, lvsa/lvsa_processor.py:798-804: 128 MB).      */
+LVSA_API int lvsa_attn_workspace_query(const lvsa_attn_args* a, int64_t* bytes);
 
 /* Gather K/V rows of whole frames into a packed buffer (dst[b, i*P + t] =
  * src[b, frames[i]*P + t]).  Replaces build_global_kv

@@ -96,6 +96,8 @@ class AttnArgs(C.Structure):
         ("rel", C.c_void_p), ("words", C.c_int32), ("R", C.c_int32), ("C", C.c_int32),
         ("q_frame0", C.c_int32),
         ("q_tok0", C.c_int64), ("k_tok0", C.c_int64),
+        ("rel_rows", C.c_int32),
+        ("workspace", C.c_void_p), ("workspace_bytes", C.c_int64),
     ]
 
 
@@ -109,6 +111,7 @@ SIGNATURES = {
     "lvsa_csr_to_bitmap": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int32, C.c_int32, C.c_void_p, C.c_int32,
                                      C.c_void_p, C.c_void_p]),
     "lvsa_attn_fwd": (C.c_int, [C.POINTER(AttnArgs), C.c_void_p]),
+    "lvsa_attn_workspace_query": (C.c_int, [C.POINTER(AttnArgs), C.POINTER(C.c_int64)]),
     "lvsa_gather_frames": (C.c_int, [C.c_void_p, C.POINTER(C.c_int64), C.c_void_p, C.POINTER(C.c_int64),
                                      C.c_void_p, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
                                      C.c_int32, C.c_void_p]),

@@ -33,7 +33,8 @@ class BlockSparseAttentionWrapper:
     """HIP block-sparse attention over a block CSR (FlashInfer-compatible subset).
 
     ``float_workspace_buffer`` is accepted for signature compatibility; the
-    kernels need no workspace beyond the plan, which lives on the device.
+    plan lives on the device, and the only scratch (for split text tiles) is
+    taken per call from torch's caching allocator.
     """
 
     def __init__(self, float_workspace_buffer: Optional[torch.Tensor] = None, backend: str = "auto"):
@@ -62,6 +63,8 @@ class BlockSparseAttentionWrapper:
             raise ValueError("num_qo_heads must be a multiple of num_kv_heads")
         if M % R or N % C:
             raise ValueError(f"M={M} / N={N} must be multiples of the block sizes R={R} / C={C}")
+        if indptr.numel() - 1 != M // R:
+            raise ValueError(f"indptr has {indptr.numel() - 1} rows, M/R = {M // R} query blocks")
         device = indptr.device if indptr.device.type == "cuda" else torch.device("cuda", torch.cuda.current_device())
         indptr = indptr.to(device)
         indices = indices.to(device)
@@ -72,6 +75,17 @@ class BlockSparseAttentionWrapper:
         self._shape = (M, N, num_qo_heads, num_kv_heads, head_dim)
         self._scale = sm_scale
         self._status = status
+        self._status_checked = False
+
+    def _check_columns(self) -> None:
+        # status[0] of csr_to_bitmap flags column ids outside [0, N/C): such a
+        # CSR names blocks that do not exist.  Read once per plan, outside
+        # stream capture (the plan is reused by every run()).
+        if self._status_checked or torch.cuda.is_current_stream_capturing():
+            return
+        if int(self._status[0].item()):
+            raise ValueError("indices hold column ids outside [0, N/C)")
+        self._status_checked = True
 
     def run(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: Optional[torch.Tensor] = None,
             lse: Optional[torch.Tensor] = None, return_lse: bool = False):
@@ -81,6 +95,7 @@ class BlockSparseAttentionWrapper:
         M, N, H, Hkv, D = self._shape
         if q.shape != (M, H, D) or k.shape != (N, Hkv, D) or v.shape != (N, Hkv, D):
             raise ValueError(f"run() shapes {tuple(q.shape)}, {tuple(k.shape)} do not match the plan {self._shape}")
+        self._check_columns()
         o, _, lse_n, _ = hip_ops.attn_fwd(q.unsqueeze(0), k.unsqueeze(0), v.unsqueeze(0), self._plan,
                                           scale=self._scale, return_lse=return_lse)
         o = o[0]

@@ -5,7 +5,71 @@
 // lvsa_attn_d192.hip and lvsa_attn_d256.hip.
 #include "lvsa_attn_kernels.h"
 
+using namespace lvsa;
+
 namespace {
+
+// Key blocks (of 64 keys) per text chunk when a text tile is split: about a
+// third of a Wan / HunyuanVideo video tile and below a CogVideoX one, so the
+// chunks fill the launch's last round at a granularity finer than a tile.
+constexpr int kTextChunkBlocks = 128;
+constexpr int kMaxTextChunks = 64;
+
+// Text chunks per text tile for the arguments (1 = no split).
+int text_chunks_of(const lvsa_attn_args* a) {
+  if (a->n_tq == 0) return 1;
+  const int64_t blocks = ceil_div(a->n_k, kBN) + ceil_div(a->n_x, kBN);
+  const int64_t c = ceil_div(blocks, kTextChunkBlocks);
+  return (int)(c < 1 ? 1 : (c > kMaxTextChunks ? kMaxTextChunks : c));
+}
+
+int64_t text_ws_bytes(const lvsa_attn_args* a, int chunks) {
+  if (a->n_tq == 0 || chunks <= 1) return 0;
+  return 4 * (text_ws_o_elems(chunks, a->B, a->H, a->n_tq, a->D) + 2LL * chunks * a->B * a->H * a->n_tq);
+}
+
+// Exact log-sum-exp merge of the text chunks (lvsa-vllm-omni/lvsa_vllm_omni/
+// flashinfer_runner.py:184-197 merges two key sets the same way): with m_c the
+// running max (log2 units), l_c the row sum and o_c the unnormalised O of
+// chunk c, O = sum_c 2^(m_c - M) o_c / sum_c 2^(m_c - M) l_c, M = max_c m_c.
+// One thread per 4 consecutive d of one (batch, head, text row).
+template <typename E>
+__global__ __launch_bounds__(256) void attn_text_merge_kernel(const float* ws, int chunks, int B, int H, int n_tq,
+                                                              int D, char* ot, int64_t s0, int64_t s1, int64_t s2,
+                                                              float* lse_t) {
+  const int g4 = D / 4;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t per_bh = (int64_t)n_tq * g4;
+  if (t >= per_bh * B * H) return;
+  const int64_t bh = t / per_bh;
+  const int row = (int)((t % per_bh) / g4), dq = (int)(t % g4);
+  const int head = (int)(bh % H), batch = (int)(bh / H);
+  const int64_t stride_c = (int64_t)B * H * n_tq;  // slots per chunk
+  const int64_t slot0 = bh * n_tq + row;
+  const float2* ml = reinterpret_cast<const float2*>(ws + text_ws_o_elems(chunks, B, H, n_tq, D));
+  float M = -INFINITY;
+  for (int c = 0; c < chunks; ++c) M = fmaxf(M, ml[c * stride_c + slot0].x);
+  float L = 0.f;
+  float4 acc = float4{0.f, 0.f, 0.f, 0.f};
+  for (int c = 0; c < chunks; ++c) {
+    const float2 mc = ml[c * stride_c + slot0];
+    const float w = __builtin_amdgcn_exp2f(mc.x - M);
+    const float4 o = *reinterpret_cast<const float4*>(ws + (c * stride_c + slot0) * D + 4 * dq);
+    L += w * mc.y;
+    acc.x += w * o.x;
+    acc.y += w * o.y;
+    acc.z += w * o.z;
+    acc.w += w * o.w;
+  }
+  const float inv = L > 0.f ? 1.0f / L : 0.f;
+  E* op = reinterpret_cast<E*>(ot + 2 * (batch * s0 + row * s1 + head * s2)) + 4 * dq;
+  op[0] = (E)(acc.x * inv);
+  op[1] = (E)(acc.y * inv);
+  op[2] = (E)(acc.z * inv);
+  op[3] = (E)(acc.w * inv);
+  if (lse_t && dq == 0)
+    lse_t[bh * n_tq + row] = L > 0.f ? (M + __log2f(L)) * 0.69314718055994530942f : -INFINITY;
+}
 
 bool aligned16(const void* ptr, const int64_t* str, int n) {
   if (((uintptr_t)ptr) % 16) return false;
@@ -15,8 +79,6 @@ bool aligned16(const void* ptr, const int64_t* str, int n) {
 }
 
 }  // namespace
-
-using namespace lvsa;
 
 extern "C" int lvsa_attn_fwd(const lvsa_attn_args* a, hipStream_t stream) {
   clear_error();
@@ -60,7 +122,24 @@ extern "C" int lvsa_attn_fwd(const lvsa_attn_args* a, hipStream_t stream) {
   LVSA_REQUIRE(a->block_q != kPPBM || (fits24(a->k_str[1]) && fits24(a->v_str[1]) &&
                                        (a->n_x == 0 || (fits24(a->kx_str[1]) && fits24(a->vx_str[1])))),
                LVSA_ERR_UNSUPPORTED, "lvsa_attn_fwd: key/value row stride of 16 MiB or more (block_q 256)");
-  const int64_t work = (int64_t)a->n_tiles * a->H * a->B;
+  // Every query row must have a relation row (generic blocks read it).
+  if (a->n_q > 0) {
+    const int64_t R = a->R > 0 ? a->R : 1;
+    const int64_t first = a->q_tok0 / R - a->q_frame0, last = (a->q_tok0 + a->n_q - 1) / R - a->q_frame0;
+    LVSA_REQUIRE(a->q_tok0 >= 0 && a->k_tok0 >= 0 && first >= 0 && last < a->rel_rows && a->rel && a->words >= 1,
+                 LVSA_ERR_INVALID_ARG,
+                 "lvsa_attn_fwd: query rows map to relation rows [%lld, %lld], the relation has %d rows",
+                 (long long)first, (long long)last, a->rel_rows);
+  }
+  const int chunks = a->workspace ? text_chunks_of(a) : 1;
+  const int64_t ws_need = text_ws_bytes(a, chunks);
+  LVSA_REQUIRE(a->workspace_bytes >= ws_need, LVSA_ERR_CAPACITY,
+               "lvsa_attn_fwd: workspace of %lld bytes < %lld needed (lvsa_attn_workspace_query)",
+               (long long)a->workspace_bytes, (long long)ws_need);
+  LVSA_REQUIRE(ws_need == 0 || ((uintptr_t)a->workspace) % 16 == 0, LVSA_ERR_INVALID_ARG,
+               "lvsa_attn_fwd: workspace must be 16-byte aligned");
+  const int64_t vwork = (int64_t)n_vt * a->H * a->B, twork = (int64_t)n_tt * chunks * a->H * a->B;
+  const int64_t work = vwork + twork;
   LVSA_REQUIRE(work < (int64_t)INT32_MAX, LVSA_ERR_INVALID_ARG, "lvsa_attn_fwd: too much work");
   if (work == 0) return LVSA_OK;
 
@@ -107,10 +186,41 @@ extern "C" int lvsa_attn_fwd(const lvsa_attn_args* a, hipStream_t stream) {
   p.q_tok0 = a->q_tok0;
   p.k_tok0 = a->k_tok0;
   p.total_work = (int)work;
+  p.n_vwork = (int)vwork;
+  p.n_twork = (int)twork;
+  p.text_chunks = chunks;
+  p.text_first = chunks == 1 ? 1 : 0;
+  p.ws = chunks > 1 ? (float*)a->workspace : nullptr;
   const int bq = a->block_q;
-  if (a->D == 256) return launch_d256(p, bq, a->dtype == LVSA_BF16, stream);
-  if (a->D == 128) return launch_d128(p, bq, a->dtype == LVSA_BF16, stream);
-  if (a->D == 96) return launch_d96(p, bq, a->dtype == LVSA_BF16, stream);
-  if (a->D == 192) return launch_d192(p, bq, a->dtype == LVSA_BF16, stream);
-  return launch_d64(p, bq, a->dtype == LVSA_BF16, stream);
+  const bool bf16 = a->dtype == LVSA_BF16;
+  int rc;
+  if (a->D == 256) rc = launch_d256(p, bq, bf16, stream);
+  else if (a->D == 128) rc = launch_d128(p, bq, bf16, stream);
+  else if (a->D == 96) rc = launch_d96(p, bq, bf16, stream);
+  else if (a->D == 192) rc = launch_d192(p, bq, bf16, stream);
+  else rc = launch_d64(p, bq, bf16, stream);
+  if (rc != LVSA_OK || chunks == 1) return rc;
+  const int64_t threads = (int64_t)a->B * a->H * a->n_tq * (a->D / 4);
+  const dim3 grid((unsigned)ceil_div(threads, 256));
+  if (bf16) {
+    hipLaunchKernelGGL(attn_text_merge_kernel<__bf16>, grid, dim3(256), 0, stream, (const float*)a->workspace,
+                       chunks, a->B, a->H, a->n_tq, a->D, (char*)a->ot, a->ot_str[0], a->ot_str[1], a->ot_str[2],
+                       a->lse_t);
+  } else {
+    hipLaunchKernelGGL(attn_text_merge_kernel<_Float16>, grid, dim3(256), 0, stream, (const float*)a->workspace,
+                       chunks, a->B, a->H, a->n_tq, a->D, (char*)a->ot, a->ot_str[0], a->ot_str[1], a->ot_str[2],
+                       a->lse_t);
+  }
+  return launch_status("lvsa_attn_fwd (text merge)");
+}
+
+extern "C" int lvsa_attn_workspace_query(const lvsa_attn_args* a, int64_t* bytes) {
+  clear_error();
+  LVSA_REQUIRE(a != nullptr && bytes != nullptr, LVSA_ERR_INVALID_ARG, "lvsa_attn_workspace_query: null pointer");
+  LVSA_REQUIRE(a->n_k >= 0 && a->n_x >= 0 && a->n_tq >= 0 && a->B >= 1 && a->H >= 1, LVSA_ERR_INVALID_ARG,
+               "lvsa_attn_workspace_query: bad sizes");
+  LVSA_REQUIRE(a->D == 64 || a->D == 96 || a->D == 128 || a->D == 192 || a->D == 256, LVSA_ERR_UNSUPPORTED,
+               "lvsa_attn_workspace_query: head_dim %d not supported", a->D);
+  *bytes = text_ws_bytes(a, text_chunks_of(a));
+  return LVSA_OK;
 }

@@ -61,7 +61,20 @@ struct AttnParams {
   int words, R, C, q_frame0;
   int64_t q_tok0, k_tok0;
   int total_work;
+  // Work items: n_vwork video tiles (n_vt per head) and n_twork text items
+  // (n_tt tiles per head, each split into text_chunks key ranges).  Unsplit
+  // text tiles (text_chunks == 1) are the longest items and go first; split
+  // ones go last, where their chunks fill the launch's final round, and write
+  // unnormalised partials to ws for attn_text_merge_kernel.
+  int n_vwork, n_twork, text_chunks, text_first;
+  float* ws;
 };
+
+// Layout of the text-split scratch: O partials [chunk][B][H][n_tq][D] fp32,
+// then (running max in log2 units, row sum) pairs [chunk][B][H][n_tq].
+__host__ __device__ inline int64_t text_ws_o_elems(int chunks, int B, int H, int n_tq, int D) {
+  return (int64_t)chunks * B * H * n_tq * D;
+}
 
 // Launches per head size (bf16 / fp16), each compiled in its own translation
 // unit (lvsa_attn_d<D>.hip): the compiler's code for one head size then does
@@ -196,6 +209,91 @@ __device__ __forceinline__ void wait_vm0() {
   __builtin_amdgcn_s_waitcnt(0x0F70);
 }
 
+// The work item of this work-group.  Video tiles are remapped so that
+// consecutive tiles of one head run on one XCD (work-groups are dispatched to
+// the 8 XCDs round-robin, and each XCD has its own L2): XCD x takes a
+// contiguous range of the video items.  Text items keep the dispatch order.
+struct WorkItem {
+  int tile, head, batch, chunk;
+  bool text;
+};
+__device__ __forceinline__ WorkItem map_work(const AttnParams& p) {
+  WorkItem it;
+  const int b = blockIdx.x;
+  const int tb0 = p.text_first ? 0 : p.n_vwork;  // first block of the text items
+  const int vb0 = p.text_first ? p.n_twork : 0;  // first block of the video items
+  if (b >= tb0 && b < tb0 + p.n_twork) {
+    int t = b - tb0;
+    it.chunk = t % p.text_chunks;
+    t /= p.text_chunks;
+    it.tile = p.n_vt + t % p.n_tt;
+    t /= p.n_tt;
+    it.head = t % p.H;
+    it.batch = t / p.H;
+    it.text = true;
+    return it;
+  }
+  const int x = b % kXcds;
+  const int per = p.n_vwork / kXcds, rem = p.n_vwork % kXcds;
+  // video items on XCD y: per, plus one for the first `rem` XCDs in dispatch
+  // order after block vb0
+  int start = 0;
+  for (int y = 0; y < x; ++y) start += per + ((((y - vb0) % kXcds + kXcds) % kXcds) < rem ? 1 : 0);
+  const int first = vb0 + (((x - vb0) % kXcds + kXcds) % kXcds);  // first video block on XCD x
+  const int w = start + (b - first) / kXcds;
+  it.tile = w % p.n_vt;
+  const int rest = w / p.n_vt;
+  it.head = rest % p.H;
+  it.batch = rest / p.H;
+  it.chunk = 0;
+  it.text = false;
+  return it;
+}
+
+// Epilogue of a text chunk: the unnormalised O row of this lane (d = 32*dt +
+// 8*rq + 4*h .. +3 in oacc[dt][4*rq ..]) to `wo` (fp32), and the (running
+// max, row sum) pair to `ml`, in the scratch layout of text_ws_o_elems.
+template <int NT>
+__device__ __forceinline__ void store_text_partial(char* wo, float* ml, int h, const floatx16* oacc, float m_run,
+                                                   float l_tot) {
+#pragma unroll
+  for (int dt = 0; dt < NT; ++dt) {
+#pragma unroll
+    for (int rq = 0; rq < 4; ++rq) {
+      const int d0 = 32 * dt + 8 * rq + 4 * h;
+      *reinterpret_cast<float4*>(wo + 4 * d0) =
+          float4{oacc[dt][4 * rq], oacc[dt][4 * rq + 1], oacc[dt][4 * rq + 2], oacc[dt][4 * rq + 3]};
+    }
+  }
+  if (h == 0) *reinterpret_cast<float2*>(ml) = float2{m_run, l_tot};
+}
+
+// A split text item writes its partials where a tile writes its output: the
+// row base, row stride and LSE pointer of the text branch are redirected to
+// the scratch slots of (chunk, batch, head) (no extra state stays live
+// through the key loop).
+template <int D>
+__device__ __forceinline__ void text_partial_dst(const AttnParams& p, const WorkItem& it, char*& obase,
+                                                 int64_t& ors, float*& lse) {
+  const int64_t slot = (((int64_t)it.chunk * p.B + it.batch) * p.H + it.head) * p.n_tq;
+  obase = reinterpret_cast<char*>(p.ws + slot * D);
+  ors = 4 * D;
+  lse = p.ws + text_ws_o_elems(p.text_chunks, p.B, p.H, p.n_tq, D) + 2 * slot;
+}
+
+// Entry range [e0, e1) of the work item: the tile's plan entries, or chunk
+// `chunk` of text_chunks equal parts of them.
+__device__ __forceinline__ void item_entries(const AttnParams& p, const WorkItem& it, int& e0, int& e1) {
+  e0 = p.tile_indptr[it.tile];
+  e1 = p.tile_indptr[it.tile + 1];
+  if (it.text && p.text_chunks > 1) {
+    const int len = (e1 - e0 + p.text_chunks - 1) / p.text_chunks;
+    const int a = e0 + it.chunk * len;
+    e0 = a < e1 ? a : e1;
+    e1 = e0 + len < e1 ? e0 + len : e1;
+  }
+}
+
 template <int D, typename E>
 // Two work-groups per CU, except at D = 192 and 256 (their O and Q fragments
 // alone take up to 192 registers per lane, and a 128 KiB LDS ring leaves room
@@ -224,20 +322,9 @@ __global__ __launch_bounds__(kThreads, D >= 192 ? 1 : 2) void attn_fwd_kernel(At
   const int h = lane >> 5;        // half of the wave
   const int i32 = lane & 31;      // query row of this lane within the wave
 
-  // XCD-aware work order: consecutive work items stay on one XCD (shared L2).
-  int w;
-  {
-    const int b = blockIdx.x;
-    const int per = p.total_work / kXcds, rem = p.total_work % kXcds;
-    const int x = b % kXcds, idx = b / kXcds;
-    w = x * per + (x < rem ? x : rem) + idx;
-  }
-  const int tslot = w % p.n_tiles;
-  const int rest = w / p.n_tiles;
-  const int head = rest % p.H;
-  const int batch = rest / p.H;
-  const int tile = tslot < p.n_tt ? p.n_vt + tslot : tslot - p.n_tt;  // text tiles (longest) first
-  const bool text = tile >= p.n_vt;
+  const WorkItem it = map_work(p);
+  const int tile = it.tile, head = it.head, batch = it.batch;
+  const bool text = it.text;
   const int hk = head / p.group;
 
   const char* qbase;
@@ -262,8 +349,11 @@ __global__ __launch_bounds__(kThreads, D >= 192 ? 1 : 2) void attn_fwd_kernel(At
     nrows = p.n_tq;
     r0 = (int64_t)(tile - p.n_vt) * kBM;
     lse = p.lse_t ? p.lse_t + ((int64_t)batch * p.H + head) * p.n_tq : nullptr;
+    if (p.text_chunks > 1) text_partial_dst<D>(p, it, obase, ors, lse);
   }
-  const int e0 = p.tile_indptr[tile], e1 = p.tile_indptr[tile + 1];
+  const bool partial = text && p.text_chunks > 1;
+  int e0, e1;
+  item_entries(p, it, e0, e1);
 
   // Key sources: 0 = frame-structured key/value, 1 = dense extra rows.
   const char* kb0 = p.k + 2 * (batch * p.k_str[0] + hk * p.k_str[2]);
@@ -581,7 +671,9 @@ __global__ __launch_bounds__(kThreads, D >= 192 ? 1 : 2) void attn_fwd_kernel(At
   // Epilogue: combine the row sum of both halves, normalise, store.
   const float l_run = (l4[0] + l4[1]) + (l4[2] + l4[3]);
   const float l_tot = l_run + __shfl_xor(l_run, 32);
-  if (my_row < nrows) {
+  if (my_row < nrows && partial) {
+    store_text_partial<NT>(obase + my_row * ors, lse + 2 * my_row, h, oacc, m_run, l_tot);
+  } else if (my_row < nrows) {
     const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
     char* op = obase + my_row * ors;
 #pragma unroll
@@ -699,20 +791,9 @@ __global__ __launch_bounds__(kPPThreads, 1) void attn_fwd_pp_kernel(AttnParams p
   const int h = lane >> 5;
   const int i32 = lane & 31;
 
-  // XCD-aware work order: consecutive work items stay on one XCD (shared L2).
-  int w;
-  {
-    const int b = blockIdx.x;
-    const int per = p.total_work / kXcds, rem = p.total_work % kXcds;
-    const int x = b % kXcds, idx = b / kXcds;
-    w = x * per + (x < rem ? x : rem) + idx;
-  }
-  const int tslot = w % p.n_tiles;
-  const int rest = w / p.n_tiles;
-  const int head = rest % p.H;
-  const int batch = rest / p.H;
-  const int tile = tslot < p.n_tt ? p.n_vt + tslot : tslot - p.n_tt;  // text tiles (longest) first
-  const bool text = tile >= p.n_vt;
+  const WorkItem it = map_work(p);
+  const int tile = it.tile, head = it.head, batch = it.batch;
+  const bool text = it.text;
   const int hk = head / p.group;
 
   const char* qbase;
@@ -737,8 +818,11 @@ __global__ __launch_bounds__(kPPThreads, 1) void attn_fwd_pp_kernel(AttnParams p
     nrows = p.n_tq;
     r0 = (int64_t)(tile - p.n_vt) * kPPBM;
     lse = p.lse_t ? p.lse_t + ((int64_t)batch * p.H + head) * p.n_tq : nullptr;
+    if (p.text_chunks > 1) text_partial_dst<D>(p, it, obase, ors, lse);
   }
-  const int e0 = p.tile_indptr[tile], e1 = p.tile_indptr[tile + 1];
+  const bool partial = text && p.text_chunks > 1;
+  int e0, e1;
+  item_entries(p, it, e0, e1);
   const int n = e1 - e0;
 
   const char* kb0 = p.k + 2 * (batch * p.k_str[0] + hk * p.k_str[2]);
@@ -1217,7 +1301,9 @@ __global__ __launch_bounds__(kPPThreads, 1) void attn_fwd_pp_kernel(AttnParams p
   // Epilogue: combine the row sum of both halves, normalise, store.
   const float l_run = (l4[0] + l4[1]) + (l4[2] + l4[3]);
   const float l_tot = sum_halves(l_run);
-  if (my_row < nrows) {
+  if (my_row < nrows && partial) {
+    store_text_partial<NT>(obase + my_row * ors, lse + 2 * my_row, h, oacc, m_run, l_tot);
+  } else if (my_row < nrows) {
     const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
     char* op = obase + my_row * ors;
 #pragma unroll

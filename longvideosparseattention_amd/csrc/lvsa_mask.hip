@@ -509,6 +509,13 @@ static int plan_ctx(const lvsa_plan_params* p, PlanCtx* c) {
   LVSA_REQUIRE(p->n_q == 0 || (p->R >= 1 && p->C >= 1 && p->rel != nullptr && p->words >= 1 && p->rel_rows >= 1),
                LVSA_ERR_INVALID_ARG, "lvsa_plan: video rows need a relation (R, C, rel, words, rel_rows)");
   LVSA_REQUIRE(p->q_tok0 >= 0 && p->k_tok0 >= 0, LVSA_ERR_INVALID_ARG, "lvsa_plan: negative token offset");
+  if (p->n_q > 0) {
+    // every query row needs a relation row: rows outside it would attend nothing
+    const int64_t first = p->q_tok0 / p->R - p->q_frame0, last = (p->q_tok0 + p->n_q - 1) / p->R - p->q_frame0;
+    LVSA_REQUIRE(first >= 0 && last < p->rel_rows, LVSA_ERR_INVALID_ARG,
+                 "lvsa_plan: query rows map to relation rows [%lld, %lld], the relation has %d rows",
+                 (long long)first, (long long)last, p->rel_rows);
+  }
   c->p = *p;
   c->n_vt = (int)ceil_div(p->n_q, p->block_q);
   c->n_tt = (int)ceil_div(p->n_tq, p->block_q);

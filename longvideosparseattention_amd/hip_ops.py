@@ -150,6 +150,7 @@ class BlockPlan:
     n_video_tiles: int
     params: capi.PlanParams
     rel: Optional[torch.Tensor]  # keeps the relation bitmap alive
+    _verified: bool = False
 
     @property
     def block_q(self) -> int:
@@ -158,6 +159,22 @@ class BlockPlan:
     @property
     def block_k(self) -> int:
         return self.params.block_k
+
+    def verify(self) -> None:
+        """Raise if the plan overflowed its entry capacity (``status[0]``).
+
+        Checked once, at the first use outside stream capture (one host
+        synchronisation per plan; plans are cached and reused by every layer).
+        The capacity comes from ``max_row_frames``: a value below the
+        relation's true row maximum would otherwise truncate the key lists."""
+        if self._verified or torch.cuda.is_current_stream_capturing():
+            return
+        overflow, total = (int(x) for x in self.status[:2].tolist())
+        if overflow:
+            raise RuntimeError(
+                f"lvsa_plan_build: {total} block entries exceed the capacity {self.entries.shape[0]} "
+                f"(max_row_frames below the relation's row maximum)")
+        self._verified = True
 
 
 def plan_build(rel: Optional[torch.Tensor], *, n_q: int, n_k: int, n_x: int = 0, n_tq: int = 0,
@@ -221,11 +238,14 @@ def attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, plan: BlockPlan,
              kx: Optional[torch.Tensor] = None, vx: Optional[torch.Tensor] = None,
              qt: Optional[torch.Tensor] = None, scale: Optional[float] = None,
              return_lse: bool = False, out: Optional[torch.Tensor] = None,
-             out_t: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, Optional[torch.Tensor],
-                                                           Optional[torch.Tensor], Optional[torch.Tensor]]:
+             out_t: Optional[torch.Tensor] = None, text_split: bool = True
+             ) -> Tuple[torch.Tensor, Optional[torch.Tensor], Optional[torch.Tensor], Optional[torch.Tensor]]:
     """Block-sparse attention over ``plan``: returns ``(o, o_text, lse, lse_text)``.
 
     ``lse`` is the natural-log log-sum-exp ``[B, H, S]`` (fp32) when requested.
+    ``text_split`` passes the scratch that lets long text-query tiles run as
+    key-range chunks merged by log-sum-exp (the default); ``False`` runs each
+    text tile as one work-group.
     """
     dtype = q.dtype
     if dtype not in _DTYPES:
@@ -258,6 +278,9 @@ def attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, plan: BlockPlan,
     else:
         qt = None
     pp = plan.params
+    if plan.block_k != capi.ATTN_BLOCK_K:
+        raise ValueError(f"plan built with block_k={plan.block_k}; the attention kernels walk key blocks of "
+                         f"{capi.ATTN_BLOCK_K} rows")
     if (pp.n_q, pp.n_k, pp.n_x, pp.n_tq) != (n_q, k.shape[1], n_x, n_tq):
         raise ValueError(
             f"plan built for (n_q, n_k, n_x, n_tq)={(pp.n_q, pp.n_k, pp.n_x, pp.n_tq)}, "
@@ -287,6 +310,15 @@ def attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, plan: BlockPlan,
     a.rel = pp.rel
     a.words, a.R, a.C, a.q_frame0 = pp.words, pp.R, pp.C, pp.q_frame0
     a.q_tok0, a.k_tok0 = pp.q_tok0, pp.k_tok0
+    a.rel_rows = pp.rel_rows
+    plan.verify()
+    ws_bytes = C.c_int64(0)
+    capi.check("lvsa_attn_workspace_query", capi.lib().lvsa_attn_workspace_query(C.byref(a), C.byref(ws_bytes)))
+    ws = None
+    if ws_bytes.value > 0 and text_split:
+        # text-tile split scratch: partial O / (max, sum) per chunk, merged in the same call
+        ws = torch.empty(ws_bytes.value, dtype=torch.uint8, device=q.device)
+        a.workspace, a.workspace_bytes = ws.data_ptr(), ws_bytes.value
     with torch.cuda.device(q.device):
         capi.check("lvsa_attn_fwd", capi.lib().lvsa_attn_fwd(C.byref(a), _stream(q.device)))
     return out, out_t, lse, lse_t

@@ -481,6 +481,16 @@ def _compute_dtype(t: torch.Tensor) -> torch.dtype:
     return t.dtype if t.dtype in _COMPUTE_DTYPES else torch.bfloat16
 
 
+def _check_local_seq(query: torch.Tensor, metadata: LVSAMetadata) -> None:
+    # The metadata's relation has one row per local frame; the kernels map
+    # query row r to frame (global_token_start + r) // P, so the query length
+    # must be the metadata's local sequence (the reference slices
+    # metadata.local_frames out of it, lvsa/sparse_attention.py:668-675).
+    if query.dim() != 4 or query.shape[1] != metadata.local_seq:
+        raise ValueError(f"query has shape {tuple(query.shape)}; the metadata describes [B, "
+                         f"local_seq={metadata.local_seq}, H, D]")
+
+
 def _as(t: Optional[torch.Tensor], dtype: torch.dtype) -> Optional[torch.Tensor]:
     return None if t is None or t.dtype == dtype else t.to(dtype)
 
@@ -507,6 +517,7 @@ def lvsa_sdpa(
     Returns a new tensor with the dtype of ``query`` (fp32 callers are
     computed in bf16 and cast back).
     """
+    _check_local_seq(query, metadata)
     hip_ops._require_device(query, "query")
     dt = _compute_dtype(query)
     plan = metadata.window_plan(query.device, query.shape[1], key.shape[1], k_global.shape[1], query.shape[-1])
@@ -590,6 +601,7 @@ def lvsa_attention(
     Returns ``out`` or ``(out, out_text)`` when ``q_text`` is given; with
     ``return_lse`` the natural-log LSE ``[B, H, S]`` tensors are appended.
     """
+    _check_local_seq(query, metadata)
     hip_ops._require_device(query, "query")
     dt = _compute_dtype(query)
     n_tk = 0 if k_text is None else k_text.shape[1]

@@ -102,3 +102,56 @@ def test_attn_rejects_bad_args_without_launching():
     assert b"head_dim 192 runs 128-row tiles" in lib.lvsa_last_error()
     a.D, a.H, a.Hkv = 128, 3, 2
     assert lib.lvsa_attn_fwd(C.byref(a), None) == -1
+
+
+def _attn_args(n_q=1000, rel_rows=10, n_tq=0, n_k=1000):
+    """Arguments that pass every check up to the relation bound (fake,
+    aligned, non-null device pointers: nothing is launched by these tests)."""
+    a = _capi.AttnArgs()
+    a.D, a.dtype, a.B, a.H, a.Hkv, a.block_q = 128, 0, 1, 2, 2, 256
+    a.n_q, a.n_k, a.n_tq = n_q, n_k, n_tq
+    a.n_video_tiles = -(-n_q // 256)
+    a.n_tiles = a.n_video_tiles + -(-n_tq // 256)
+    for f in ("q", "k", "v", "o", "qt", "ot", "tile_indptr", "entries", "rel"):
+        setattr(a, f, 4096)
+    for f in ("q_str", "k_str", "v_str", "o_str", "qt_str", "ot_str"):
+        setattr(a, f, _capi._Str3(1 << 20, 256, 128))
+    a.words, a.R, a.C, a.rel_rows = 1, 100, 100, rel_rows
+    return a
+
+
+def test_attn_rejects_query_rows_outside_relation():
+    lib = _capi.lib()
+    a = _attn_args(n_q=1000, rel_rows=9)   # rows 0..999 need relation rows 0..9
+    assert lib.lvsa_attn_fwd(C.byref(a), None) == -1
+    assert b"relation rows [0, 9]" in lib.lvsa_last_error()
+    a.q_frame0 = 1                          # first query row maps to relation row -1
+    a.rel_rows = 11
+    assert lib.lvsa_attn_fwd(C.byref(a), None) == -1
+    assert b"relation rows [-1, 8]" in lib.lvsa_last_error()
+
+
+def test_attn_workspace_query_and_capacity():
+    lib = _capi.lib()
+    a = _attn_args(n_q=1000, rel_rows=10, n_tq=100, n_k=20000)
+    n = C.c_int64(-1)
+    assert lib.lvsa_attn_workspace_query(C.byref(a), C.byref(n)) == 0
+    chunks = -(-(-(-20000 // 64)) // 128)           # 313 key blocks in chunks of 128
+    assert chunks == 3
+    assert n.value == 4 * chunks * 2 * 100 * (128 + 2)
+    a.workspace, a.workspace_bytes = 4096, n.value - 16
+    assert lib.lvsa_attn_fwd(C.byref(a), None) == -3
+    assert b"workspace" in lib.lvsa_last_error()
+    b = _attn_args(n_q=1000, rel_rows=10)     # no text queries: no scratch
+    assert lib.lvsa_attn_workspace_query(C.byref(b), C.byref(n)) == 0 and n.value == 0
+
+
+def test_plan_rejects_query_rows_outside_relation():
+    lib = _capi.lib()
+    p = _capi.PlanParams(n_q=1000, n_k=1000, n_x=0, n_tq=0, R=100, C=100, q_tok0=0, k_tok0=0,
+                         q_frame0=0, rel_rows=9, words=1, rel=4096, block_q=256, block_k=64)
+    s = _capi.PlanSizes()
+    assert lib.lvsa_plan_sizes_query(C.byref(p), 5, C.byref(s)) == -1
+    assert b"relation rows [0, 9]" in lib.lvsa_last_error()
+    p.rel_rows = 10
+    assert lib.lvsa_plan_sizes_query(C.byref(p), 5, C.byref(s)) == 0

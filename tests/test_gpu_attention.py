@@ -367,3 +367,77 @@ def test_baseline_config_parity(cfg, gpu):
         rto, _ = oa.text_row_attention(qt.to(gpu).float(), kd.float(), vd.float(), kt.to(gpu).float(),
                                        vt.to(gpu).float())
         _close(ot, rto, name + " text rows")
+
+
+SPLIT = [
+    # T, P, H, Hkv, D, n_txt, dtype, B   (text tiles of more than 128 key blocks: split into chunks)
+    (8, 1100, 2, 2, 128, 100, torch.bfloat16, 1),   # 141 blocks: 2 chunks
+    (24, 1100, 2, 1, 128, 300, torch.bfloat16, 2),  # 418 blocks: 4 chunks, GQA, batch 2
+    (13, 1350, 3, 3, 64, 226, torch.float16, 1),    # CogVideoX frame size
+    (9, 1000, 2, 2, 96, 37, torch.bfloat16, 1),
+    (9, 1000, 2, 2, 256, 37, torch.bfloat16, 1),    # 128-row tiles
+]
+
+
+@pytest.mark.parametrize("cfg", SPLIT, ids=[str(c[:6]) for c in SPLIT])
+def test_text_split_parity(cfg, gpu):
+    """Text-query tiles split into key-range chunks (scratch + log-sum-exp
+    merge launch) against the fp32 oracle and against the unsplit launch."""
+    T, P, H, Hkv, D, n_txt, dt, B = cfg
+    N = T * P
+    m = _meta(T, P, 1, 1, 4, 1)
+    q, k, v, qt, kt, vt = _draw([(B, N, H, D), (B, N, Hkv, D), (B, N, Hkv, D), (B, n_txt, H, D),
+                                 (B, n_txt, Hkv, D), (B, n_txt, Hkv, D)], seed=3, dtype=dt)
+    g = [x.to(gpu) for x in (q, k, v, qt, kt, vt)]
+    plan = m.full_plan(gpu, N, N, n_txt, n_txt, D)
+    o1, ot1, l1, lt1 = hip_ops.attn_fwd(g[0], g[1], g[2], plan, kx=g[4], vx=g[5], qt=g[3], return_lse=True)
+    o0, ot0, l0, lt0 = hip_ops.attn_fwd(g[0], g[1], g[2], plan, kx=g[4], vx=g[5], qt=g[3], return_lse=True,
+                                        text_split=False)
+    assert torch.equal(o1, o0) and torch.equal(l1, l0)   # video rows do not depend on the split
+    for b in range(B):
+        rto, rtl = oa.text_row_attention(qt[b:b + 1].float(), k[b:b + 1].float(), v[b:b + 1].float(),
+                                         kt[b:b + 1].float(), vt[b:b + 1].float())
+        _close(ot1[b:b + 1], rto, f"split text rows, batch {b}")
+        _close(ot0[b:b + 1], rto, f"unsplit text rows, batch {b}")
+        torch.testing.assert_close(lt1[b:b + 1].cpu(), rtl, atol=2e-2, rtol=0)
+    _close(ot1, ot0.float(), "split vs unsplit", max_abs=8e-3, mean_abs=5e-4)
+
+
+def test_single_prefill_long_keys_split(gpu):
+    """Dense prefill over more than 128 key blocks runs split (chunks + merge)."""
+    q, k, v = (x.to(gpu) for x in _draw([(1, 70, 4, 128), (1, 20000, 2, 128), (1, 20000, 2, 128)], seed=5))
+    o, lse = lv.single_prefill_with_kv_cache(q[0], k[0], v[0], causal=False, return_lse=True)
+    ro, rl = oa.dense_attention(q.float(), k.float(), v.float())
+    _close(o.unsqueeze(0), ro, "single_prefill split")
+    torch.testing.assert_close(lse.cpu(), rl[0].transpose(0, 1).cpu() / math.log(2.0), atol=3e-2, rtol=0)
+
+
+def test_plan_overflow_and_block_k_are_rejected(gpu):
+    """A plan whose entry capacity is too small (max_row_frames below the
+    relation's row maximum) raises at first use; so does a plan built for key
+    blocks other than the kernels' 64 rows."""
+    T, P, H, D = 12, 300, 2, 128
+    m = _meta(T, P, 2, 1, 4, 1)
+    m.ensure_device(gpu)
+    st = m.device_state(gpu)
+    q, k, v = (x.to(gpu) for x in _draw([(1, T * P, H, D)] * 3))
+    bad = hip_ops.plan_build(st.mask.rel_full, n_q=T * P, n_k=T * P, R=P, Cf=P, max_row_frames=1)
+    with pytest.raises(RuntimeError, match="exceed the capacity"):
+        hip_ops.attn_fwd(q, k, v, bad)
+    wide = hip_ops.plan_build(st.mask.rel_full, n_q=T * P, n_k=T * P, R=P, Cf=P,
+                              max_row_frames=m.max_row_frames, block_k=128)
+    with pytest.raises(ValueError, match="block_k=128"):
+        hip_ops.attn_fwd(q, k, v, wide)
+    good = hip_ops.plan_build(st.mask.rel_full, n_q=T * P, n_k=T * P, R=P, Cf=P, max_row_frames=m.max_row_frames)
+    out, _, _, _ = hip_ops.attn_fwd(q, k, v, good)
+    assert torch.equal(out, lv.lvsa_attention(q, k, v, m))
+
+
+def test_wrapper_rejects_out_of_range_columns(gpu):
+    w = lv.BlockSparseAttentionWrapper()
+    indptr = torch.tensor([0, 2, 3], dtype=torch.int32)
+    indices = torch.tensor([0, 5, 1], dtype=torch.int32)  # column 5 of 2
+    w.plan(indptr, indices, M=128, N=128, R=64, C=64, num_qo_heads=2, num_kv_heads=2, head_dim=128)
+    q, k, v = (x.to(gpu) for x in _draw([(128, 2, 128)] * 3))
+    with pytest.raises(ValueError, match="outside"):
+        w.run(q, k, v)

@@ -152,3 +152,24 @@ def test_head_sizes_of_the_plugin():
     assert hip_ops.attn_block_q(96) == 256
     with pytest.raises(ValueError, match="head_dim 80"):
         hip_ops.kernel_head_dim(80)
+
+
+def test_query_length_must_match_metadata():
+    """The kernels map query row r to local frame (start + r) // P: a query
+    that is not the metadata's local sequence is rejected before any device
+    work (the reference slices metadata.local_frames out of the query)."""
+    m = lv.LVSAMetadata.build(total_latent_frames=5, num_patches=4, window_size=1, n_first_frames=1,
+                              key_frame_interval=None, rank=0, world=1)
+    q = torch.randn(1, 16, 2, 64)     # 4 frames of 4, metadata has 5
+    with pytest.raises(ValueError, match="local_seq=20"):
+        lv.lvsa_sdpa(q, q, q, q[:, :4], q[:, :4], m)
+    with pytest.raises(ValueError, match="local_seq=20"):
+        lv.lvsa_attention(q, q, q, m)
+
+
+def test_wrapper_rejects_csr_with_wrong_row_count():
+    w = lv.BlockSparseAttentionWrapper()
+    indptr = torch.tensor([0, 1, 2], dtype=torch.int32)      # 2 rows, M/R = 3
+    indices = torch.tensor([0, 1], dtype=torch.int32)
+    with pytest.raises(ValueError, match="M/R = 3"):
+        w.plan(indptr, indices, M=192, N=128, R=64, C=64, num_qo_heads=2, num_kv_heads=2, head_dim=128)
