@@ -213,6 +213,19 @@ LVSA_API int lvsa_attn_fwd(const lvsa_attn_args* a, hipStream_t stream);
  * (flashinfer_runner.py:75-79, lvsa/lvsa_processor.py:798-804: 128 MB).      */
 LVSA_API int lvsa_attn_workspace_query(const lvsa_attn_args* a, int64_t* bytes);
 
+/* lvsa_attn_fwd without any allocation, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  It has no counterpart in the reference.  The
+ * scratch of the text-tile split comes from a static device array of
+ * LVSA_NOALLOC_SCRATCH_BYTES per GPU (a->workspace is ignored), which each GPU
+ * the library runs on holds until the process ends; a call that needs more
+ * returns LVSA_ERR_CAPACITY.  All calls on one GPU share that array: calls
+ * that overlap on one GPU (other streams, other threads) race, so serialise
+ * them.  The caller still passes inputs and outputs; nothing else differs
+ * from lvsa_attn_fwd.                                                         */
+#define LVSA_NOALLOC_SCRATCH_BYTES (64LL << 20)
+LVSA_API int lvsa_attn_fwd_noalloc(const lvsa_attn_args* a, hipStream_t stream);
+
 /* Gather K/V rows of whole frames into a packed buffer (dst[b, i*P + t] =
  * src[b, frames[i]*P + t]).  Replaces build_global_kv
  * (lvsa-vllm-omni/lvsa_vllm_omni/global_kv.py:12-42) and the single-GPU copy

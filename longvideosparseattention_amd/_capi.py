@@ -24,6 +24,8 @@ STATUS = {0: "ok", -1: "invalid argument", -2: "unsupported", -3: "capacity", -4
 # Kernel tiling of lvsa_attn_fwd (query rows x key rows per block).
 ATTN_BLOCK_Q = 128
 ATTN_BLOCK_K = 64
+# Static scratch of lvsa_attn_fwd_noalloc (LVSA_NOALLOC_SCRATCH_BYTES).
+NOALLOC_SCRATCH_BYTES = 64 << 20
 
 
 class LvsaError(RuntimeError):
@@ -112,6 +114,7 @@ SIGNATURES = {
                                      C.c_void_p, C.c_void_p]),
     "lvsa_attn_fwd": (C.c_int, [C.POINTER(AttnArgs), C.c_void_p]),
     "lvsa_attn_workspace_query": (C.c_int, [C.POINTER(AttnArgs), C.POINTER(C.c_int64)]),
+    "lvsa_attn_fwd_noalloc": (C.c_int, [C.POINTER(AttnArgs), C.c_void_p]),
     "lvsa_gather_frames": (C.c_int, [C.c_void_p, C.POINTER(C.c_int64), C.c_void_p, C.POINTER(C.c_int64),
                                      C.c_void_p, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
                                      C.c_int32, C.c_void_p]),

@@ -5,6 +5,8 @@
 // lvsa_attn_d192.hip and lvsa_attn_d256.hip.
 #include "lvsa_attn_kernels.h"
 
+#include <mutex>
+
 using namespace lvsa;
 
 namespace {
@@ -69,6 +71,32 @@ __global__ __launch_bounds__(256) void attn_text_merge_kernel(const float* ws, i
   op[3] = (E)(acc.w * inv);
   if (lse_t && dq == 0)
     lse_t[bh * n_tq + row] = L > 0.f ? (M + __log2f(L)) * 0.69314718055994530942f : -INFINITY;
+}
+
+// Scratch of lvsa_attn_fwd_noalloc: one array per GPU, held by the loaded
+// code object until the process ends.  In host code `scratch` only names the
+// symbol; its device address comes from hipGetSymbolAddress, once per device.
+__device__ __align__(256) char scratch[LVSA_NOALLOC_SCRATCH_BYTES];
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of the current device's scratch (set up on its first call).
+int scratch_of_current_device(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  LVSA_REQUIRE(e == hipSuccess, LVSA_ERR_HIP, "lvsa_attn_fwd_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+  LVSA_REQUIRE(dev >= 0 && dev < kMaxDevices, LVSA_ERR_UNSUPPORTED, "lvsa_attn_fwd_noalloc: device %d", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    LVSA_REQUIRE(e == hipSuccess && ptr != nullptr, LVSA_ERR_HIP,
+                 "lvsa_attn_fwd_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return LVSA_OK;
 }
 
 bool aligned16(const void* ptr, const int64_t* str, int n) {
@@ -223,4 +251,25 @@ extern "C" int lvsa_attn_workspace_query(const lvsa_attn_args* a, int64_t* bytes
                "lvsa_attn_workspace_query: head_dim %d not supported", a->D);
   *bytes = text_ws_bytes(a, text_chunks_of(a));
   return LVSA_OK;
+}
+
+extern "C" int lvsa_attn_fwd_noalloc(const lvsa_attn_args* a, hipStream_t stream) {
+  clear_error();
+  LVSA_REQUIRE(a != nullptr, LVSA_ERR_INVALID_ARG, "lvsa_attn_fwd_noalloc: null args");
+  int64_t need = 0;
+  int rc = lvsa_attn_workspace_query(a, &need);
+  if (rc != LVSA_OK) return rc;
+  LVSA_REQUIRE(need <= (int64_t)LVSA_NOALLOC_SCRATCH_BYTES, LVSA_ERR_CAPACITY,
+               "lvsa_attn_fwd_noalloc: the text-tile split needs %lld bytes of scratch, more than the static "
+               "%lld (LVSA_NOALLOC_SCRATCH_BYTES); call lvsa_attn_fwd with a workspace instead",
+               (long long)need, (long long)LVSA_NOALLOC_SCRATCH_BYTES);
+  lvsa_attn_args b = *a;
+  b.workspace = nullptr;
+  b.workspace_bytes = 0;
+  if (need > 0) {
+    rc = scratch_of_current_device(&b.workspace);
+    if (rc != LVSA_OK) return rc;
+    b.workspace_bytes = LVSA_NOALLOC_SCRATCH_BYTES;
+  }
+  return lvsa_attn_fwd(&b, stream);
 }

@@ -234,19 +234,25 @@ def _str3(t: Optional[torch.Tensor]):
     return capi._Str3(*(t.stride()[:3] if t is not None else (0, 0, 0)))
 
 
-def attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, plan: BlockPlan, *,
-             kx: Optional[torch.Tensor] = None, vx: Optional[torch.Tensor] = None,
-             qt: Optional[torch.Tensor] = None, scale: Optional[float] = None,
-             return_lse: bool = False, out: Optional[torch.Tensor] = None,
-             out_t: Optional[torch.Tensor] = None, text_split: bool = True
-             ) -> Tuple[torch.Tensor, Optional[torch.Tensor], Optional[torch.Tensor], Optional[torch.Tensor]]:
-    """Block-sparse attention over ``plan``: returns ``(o, o_text, lse, lse_text)``.
+@dataclass
+class AttnCall:
+    """The C-ABI arguments of one attention call and the tensors they point to
+    (repacked inputs and fresh outputs are kept alive here)."""
 
-    ``lse`` is the natural-log log-sum-exp ``[B, H, S]`` (fp32) when requested.
-    ``text_split`` passes the scratch that lets long text-query tiles run as
-    key-range chunks merged by log-sum-exp (the default); ``False`` runs each
-    text tile as one work-group.
-    """
+    args: capi.AttnArgs
+    out: torch.Tensor
+    out_t: Optional[torch.Tensor]
+    lse: Optional[torch.Tensor]
+    lse_t: Optional[torch.Tensor]
+    tensors: tuple
+
+
+def attn_args(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, plan: BlockPlan, *,
+              kx: Optional[torch.Tensor] = None, vx: Optional[torch.Tensor] = None,
+              qt: Optional[torch.Tensor] = None, scale: Optional[float] = None,
+              return_lse: bool = False, out: Optional[torch.Tensor] = None,
+              out_t: Optional[torch.Tensor] = None) -> AttnCall:
+    """Validate an attention call and fill its ``lvsa_attn_args`` (no workspace)."""
     dtype = q.dtype
     if dtype not in _DTYPES:
         raise TypeError(f"unsupported dtype {dtype}: bf16 or fp16 inputs (fp32 callers cast first)")
@@ -312,16 +318,35 @@ def attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, plan: BlockPlan,
     a.q_tok0, a.k_tok0 = pp.q_tok0, pp.k_tok0
     a.rel_rows = pp.rel_rows
     plan.verify()
+    return AttnCall(a, out, out_t, lse, lse_t, (q, k, v, kx, vx, qt, plan))
+
+
+def attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, plan: BlockPlan, *,
+             kx: Optional[torch.Tensor] = None, vx: Optional[torch.Tensor] = None,
+             qt: Optional[torch.Tensor] = None, scale: Optional[float] = None,
+             return_lse: bool = False, out: Optional[torch.Tensor] = None,
+             out_t: Optional[torch.Tensor] = None, text_split: bool = True
+             ) -> Tuple[torch.Tensor, Optional[torch.Tensor], Optional[torch.Tensor], Optional[torch.Tensor]]:
+    """Block-sparse attention over ``plan``: returns ``(o, o_text, lse, lse_text)``.
+
+    ``lse`` is the natural-log log-sum-exp ``[B, H, S]`` (fp32) when requested.
+    ``text_split`` passes the scratch that lets long text-query tiles run as
+    key-range chunks merged by log-sum-exp (the default); ``False`` runs each
+    text tile as one work-group.
+    """
+    call = attn_args(q, k, v, plan, kx=kx, vx=vx, qt=qt, scale=scale, return_lse=return_lse, out=out,
+                     out_t=out_t)
+    a = call.args
     ws_bytes = C.c_int64(0)
     capi.check("lvsa_attn_workspace_query", capi.lib().lvsa_attn_workspace_query(C.byref(a), C.byref(ws_bytes)))
     ws = None
     if ws_bytes.value > 0 and text_split:
         # text-tile split scratch: partial O / (max, sum) per chunk, merged in the same call
-        ws = torch.empty(ws_bytes.value, dtype=torch.uint8, device=q.device)
+        ws = torch.empty(ws_bytes.value, dtype=torch.uint8, device=call.out.device)
         a.workspace, a.workspace_bytes = ws.data_ptr(), ws_bytes.value
-    with torch.cuda.device(q.device):
-        capi.check("lvsa_attn_fwd", capi.lib().lvsa_attn_fwd(C.byref(a), _stream(q.device)))
-    return out, out_t, lse, lse_t
+    with torch.cuda.device(call.out.device):
+        capi.check("lvsa_attn_fwd", capi.lib().lvsa_attn_fwd(C.byref(a), _stream(call.out.device)))
+    return call.out, call.out_t, call.lse, call.lse_t
 
 
 # ───────────────────────────── frame gather ────────────────────────────────
