@@ -79,6 +79,8 @@ def _finish(proc, what, verbose):
 def build(verbose: bool = False) -> Path:
     """Compile every translation unit (in parallel) and link the shared library."""
     LIB_DIR.mkdir(exist_ok=True)
+    # the hand-scheduled key loop of the single-stream D = 128 kernel
+    subprocess.run([sys.executable, str(CSRC / "gen_stream_asm.py")], check=True)
     tmp = LIB.with_suffix(".so.tmp")
     with tempfile.TemporaryDirectory(prefix="lvsa_build_") as objdir:
         jobs = []

@@ -68,6 +68,10 @@ struct AttnParams {
   // unnormalised partials to ws for attn_text_merge_kernel.
   int n_vwork, n_twork, text_chunks, text_first;
   float* ws;
+  // D = 128, 256-row tiles: run the single-stream kernel (its loop handles
+  // descriptors "none" and "two-part", which is all such a plan holds when
+  // query frames span at least 255 rows and key frames at least 64)
+  int use_stream;
 };
 
 // Layout of the text-split scratch: O partials [chunk][B][H][n_tq][D] fp32,

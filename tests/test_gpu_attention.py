@@ -283,16 +283,20 @@ EXTREME = ["hot", "cold", "cold_then_hot", "hot_then_cold"]
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
 @pytest.mark.parametrize("D", [64, 96, 128, 192, 256])
 @pytest.mark.parametrize("pattern", EXTREME)
-def test_extreme_logits(pattern, D, dt, block_q, gpu, monkeypatch):
+@pytest.mark.parametrize("P", [96, 300])
+def test_extreme_logits(P, pattern, D, dt, block_q, gpu, monkeypatch):
     """Logits far from N(0,1), where the exponent offset of a row has to move.
 
     * hot: |s * scale| up to hundreds, so 2^(s * scale * log2 e) overflows fp32 without an offset.
     * cold: every logit very negative, so the exponentials underflow without an offset.
     * cold_then_hot / hot_then_cold: the key frames switch between the two, so a row's offset
       first settles low and must move up, or must stay while later blocks vanish.
+
+    Frames of 300 tokens put D = 128 on the single-stream kernel, whose softmax
+    skips the row max unless a block raises it (its rare path).
     """
     monkeypatch.setenv("LVSA_ATTN_BLOCK_Q", str(block_q))
-    T, P, W, n, kfi, off, H = 9, 96, 1, 1, 4, 1, 2
+    T, W, n, kfi, off, H = 9, 1, 1, 4, 1, 2
     N = T * P
     amp = 12.0 if dt == torch.bfloat16 else 5.0
     g = torch.Generator().manual_seed(7)
@@ -441,3 +445,48 @@ def test_wrapper_rejects_out_of_range_columns(gpu):
     q, k, v = (x.to(gpu) for x in _draw([(128, 2, 128)] * 3))
     with pytest.raises(ValueError, match="outside"):
         w.run(q, k, v)
+
+
+def _stream_cfg(seed):
+    """Random geometries the single-stream D = 128 kernel serves (frames of at
+    least 255 tokens): window / keyframe patterns, text, GQA, both dtypes."""
+    g = torch.Generator().manual_seed(2000 + seed)
+    pick = lambda xs: xs[int(torch.randint(len(xs), (1,), generator=g))]  # noqa: E731
+    T = int(torch.randint(1, 14, (1,), generator=g))
+    P = int(torch.randint(255, 700, (1,), generator=g))
+    W = pick([0, 1, 2, 3])
+    n = pick([1, 1, 2])
+    kfi = pick([None, 1, 2, 3, 4, 8])
+    off = int(torch.randint(0, 8, (1,), generator=g)) % (kfi or 1)
+    Hkv = pick([1, 2])
+    H = Hkv * pick([1, 2])
+    n_txt = pick([0, 0, 1, 37, 64, 300])
+    dt = pick([torch.bfloat16, torch.float16])
+    return T, P, W, n, kfi, off, H, Hkv, n_txt, dt
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_stream_kernel_random_geometries(seed, gpu, monkeypatch):
+    """D = 128 on frames of >= 255 tokens runs the hand-scheduled single-stream
+    kernel; against the fp32 oracle, and the ping-pong kernel within bf16
+    rounding."""
+    T, P, W, n, kfi, off, H, Hkv, n_txt, dt = _stream_cfg(seed)
+    N = T * P
+    m = _meta(T, P, W, n, kfi, off)
+    q, k, v, qt, kt, vt = _draw([(1, N, H, 128), (1, N, Hkv, 128), (1, N, Hkv, 128), (1, n_txt, H, 128),
+                                 (1, n_txt, Hkv, 128), (1, n_txt, Hkv, 128)], seed=seed, dtype=dt)
+    rows = [set(r) for r in om.build_frame_mask(T, P, W, n, kfi, offset=off).rows]
+    args = dict(k_text=kt.to(gpu), v_text=vt.to(gpu), q_text=qt.to(gpu)) if n_txt else {}
+    res = lv.lvsa_attention(q.to(gpu), k.to(gpu), v.to(gpu), m, return_lse=True, **args)
+    monkeypatch.setenv("LVSA_ATTN_KERNEL", "pp")
+    res_pp = lv.lvsa_attention(q.to(gpu), k.to(gpu), v.to(gpu), m, return_lse=True, **args)
+    ro, rl = oa.per_frame_sdpa(q.float(), k.float(), v.float(), rows, P,
+                               k_extra=kt.float() if n_txt else None, v_extra=vt.float() if n_txt else None)
+    what = f"seed {seed}: T={T} P={P} W={W} n={n} kfi={kfi} off={off} H={H}/{Hkv} txt={n_txt} {dt}"
+    o, lse = (res[0], res[2]) if n_txt else res
+    _close(o, ro, what)
+    torch.testing.assert_close(lse.cpu(), rl, atol=2e-2, rtol=0, msg=what)
+    _close(o, (res_pp[0] if n_txt else res_pp[0]).float(), what + " vs ping-pong", max_abs=8e-3, mean_abs=5e-4)
+    if n_txt:
+        rto, _ = oa.text_row_attention(qt.float(), k.float(), v.float(), kt.float(), vt.float())
+        _close(res[1], rto, what + " text rows")

@@ -1,0 +1,158 @@
+"""The hand-scheduled key loop of the single-stream D = 128 kernel, on the CPU.
+
+* The committed lvsa_attn_stream_body.inc is what gen_stream_asm.py generates.
+* tests/asm_sim.py runs the generated loop for the 8 waves of one 256-row
+  work-group over small K/V/Q and plans (full blocks, a key tail, text rows
+  as the extra source, two-part descriptors with a row split, the rare path
+  forced on every sub-block) and the result is compared with float64
+  attention over the keys the plan allows.  Tolerance: bf16 inputs and P,
+  fp32 accumulation: max |err| <= 4e-3, LSE within 2e-3.
+"""
+import math
+import struct
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import asm_sim as A
+
+CSRC = Path(__file__).resolve().parents[1] / "longvideosparseattention_amd" / "csrc"
+
+
+def test_committed_loop_is_generated():
+    assert (CSRC / "lvsa_attn_stream_body.inc").read_text() == A.G.render()
+
+
+def _swz(r):
+    return ((r & 3) << 2) | ((r >> 2) & 3)
+
+
+def _desc_two_part(bits, kb, qs):
+    return 1 | (bits << 2) | (kb << 8) | (qs << 16)
+
+
+def _allowed(y, row, key_in_block):
+    """Reference meaning of a plan descriptor (lvsa_amd.h)."""
+    if y & 3 == 0:
+        return True
+    bits, kb, qs = (y >> 2) & 0xF, (y >> 8) & 0xFF, (y >> 16) & 0xFF
+    part_b = row >= qs
+    lo = key_in_block < kb
+    bit = (2 if part_b else 0) + (0 if lo else 1)
+    return bool((bits >> bit) & 1)
+
+
+def run_loop(entries, nk, n_x, seed=0, dt="bf16", **opts):
+    rng = np.random.default_rng(seed)
+    D, R = 128, 256
+    rnd = (lambda x: A.bf16_to_f32(A.bf16_round(x))) if dt == "bf16" else (lambda x: x.astype(np.float16).astype(np.float32))
+    enc = (lambda x: A.bf16_round(x).astype(np.uint16).tobytes()) if dt == "bf16" else (lambda x: x.astype(np.float16).tobytes())
+    q = rnd(rng.standard_normal((R, D)).astype(np.float32))
+    k, v = (rnd(rng.standard_normal((nk, D)).astype(np.float32)) for _ in range(2))
+    kx, vx = (rnd(rng.standard_normal((max(n_x, 1), D)).astype(np.float32)) for _ in range(2))
+    sim = A.Sim(dt, **opts)
+    kb0, vb0, kb1, vb1 = (sim.mem.alloc(enc(x)) for x in (k, v, kx, vx))
+    ep = sim.mem.alloc(b"".join(struct.pack("<II", x, y) for x, y in entries))
+    scale = 1 / math.sqrt(D)
+    lane = np.arange(64)
+    h, i32 = lane >> 5, lane & 31
+    qbits = (A.bf16_round(q) if dt == "bf16" else q.astype(np.float16).view(np.uint16).astype(np.uint32))
+    waves = []
+    for w in range(8):
+        W = A.Wave(w, sim)
+        V = W.v
+        rows = 32 * w + i32
+        for c in range(8):
+            for j in range(4):
+                d0 = 16 * c + 8 * h + 2 * j
+                V[64 + 4 * c + j] = qbits[rows, d0] | (qbits[rows, d0 + 1] << 16)
+        sw = np.array([_swz(x & 15) for x in i32])
+        for c in range(8):
+            V[176 + c] = i32 * 256 + (((2 * c + h) ^ sw) << 4)
+        rowA = 4 * h + ((lane & 15) >> 2)
+        dgrp = (lane >> 4) & 1
+        for dt_ in range(4):
+            chunk = 4 * dt_ + 2 * dgrp + ((lane & 3) >> 1)
+            inb = (lane & 1) * 8
+            V[184 + dt_] = 65536 + rowA * 256 + ((chunk ^ np.array([_swz(x) for x in rowA])) << 4) + inb
+            V[188 + dt_] = 65536 + (rowA + 8) * 256 + ((chunk ^ np.array([_swz(x) for x in rowA + 8])) << 4) + inb
+        crow = 4 * w + lane // 16
+        V[196] = crow
+        V[197] = ((lane & 15) ^ np.array([_swz(x & 15) for x in crow])) * 16
+        V[200], V[201], V[202], V[203] = 32 * w + i32, 4 * h, 0xFF800000, 0
+        V[192] = A.f2u(np.full(64, -1e30, np.float32))
+        S = W.s
+        S[20], S[21], S[22] = ep & 0xFFFFFFFF, ep >> 32, len(entries)
+        S[23] = int(A.f2u(np.float32(scale * 1.4426950408889634)))
+        for i, b in enumerate((kb0, vb0, kb1, vb1)):
+            S[24 + 2 * i], S[25 + 2 * i] = b & 0xFFFFFFFF, b >> 32
+        S[32:36] = [256, 256, 256, 256]
+        S[36], S[37], S[39] = nk, n_x, 1024 * w
+        waves.append(W)
+    sim.run(waves)
+    O = np.zeros((R, D))
+    lsum, mrun = np.zeros(R), np.zeros(R)
+    for w, W in enumerate(waves):
+        for ln in range(64):
+            r, hh = 32 * w + (ln & 31), ln >> 5
+            for dt_ in range(4):
+                for rr in range(16):
+                    O[r, 32 * dt_ + 8 * (rr // 4) + 4 * hh + rr % 4] = A.u2f(W.v[16 * dt_ + rr, ln])
+            lsum[r] += A.u2f(W.v[193, ln])
+            mrun[r] = A.u2f(W.v[192, ln])
+    # reference: float64 softmax attention over the allowed keys
+    ref = np.zeros((R, D))
+    lse_ref = np.zeros(R)
+    for r in range(R):
+        ks, vs = [], []
+        for x, y in entries:
+            src_k, src_v, nn = (kx, vx, n_x) if x >> 31 else (k, v, nk)
+            j = x & 0x7FFFFFFF
+            for t in range(64 * j, min(64 * j + 64, nn)):
+                if _allowed(y, r, t - 64 * j):
+                    ks.append(src_k[t])
+                    vs.append(src_v[t])
+        s = np.asarray(ks, np.float64) @ q[r].astype(np.float64) * scale
+        p = np.exp(s - s.max())
+        ref[r] = p @ np.asarray(vs, np.float64) / p.sum()
+        lse_ref[r] = math.log(p.sum()) + s.max()
+    out = O / lsum[:, None]
+    lse = (mrun + np.log2(lsum)) * math.log(2)
+    return np.abs(out - ref).max(), np.abs(lse - lse_ref).max(), sim.copies
+
+
+def _tail(nn, j):
+    kn = min(64, nn - 64 * j)
+    return 0 if kn == 64 else _desc_two_part(0x5, kn, 255)
+
+
+CASES = {
+    "full_blocks": (lambda: [(j, 0) for j in range(3)], 192, 0),
+    "tail_and_text": (lambda: [(j, _tail(150, j)) for j in range(3)] + [(0x80000000, _tail(5, 0))], 150, 5),
+    "row_split": (lambda: [(0, 0), (1, _desc_two_part(0b1011, 40, 100)), (2, _desc_two_part(0b0110, 64, 37)),
+                           (3, _desc_two_part(0b1101, 17, 255))], 256, 0),
+    "one_block": (lambda: [(1, _tail(100, 1))], 100, 0),
+}
+
+
+@pytest.mark.parametrize("case", sorted(CASES))
+def test_loop_matches_attention(case):
+    make, nk, n_x = CASES[case]
+    entries = make()
+    err, lse_err, copies = run_loop(entries, nk, n_x)
+    assert err <= 4e-3 and lse_err <= 2e-3, (case, err, lse_err)
+    # 4 copies per wave per block for blocks 0..n+1 (the last two repeat block n-1)
+    assert copies == 8 * 4 * (len(entries) + 2)
+
+
+def test_loop_rare_path_every_sub_block():
+    """The exact-max path (rescale of O and l) on every sub-block gives the
+    same attention."""
+    err, lse_err, _ = run_loop([(j, 0) for j in range(3)], 192, 0, seed=3, always_rare=True)
+    assert err <= 4e-3 and lse_err <= 2e-3
+
+
+def test_loop_fp16():
+    err, lse_err, _ = run_loop([(j, _tail(150, j)) for j in range(3)], 150, 0, seed=4, dt="f16")
+    assert err <= 2e-3 and lse_err <= 2e-3
