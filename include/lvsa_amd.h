@@ -50,7 +50,10 @@ typedef enum lvsa_status {
   LVSA_ERR_HIP = -4            /* a HIP runtime call failed (launch error)        */
 } lvsa_status;
 
-typedef enum lvsa_dtype { LVSA_BF16 = 0, LVSA_FP16 = 1 } lvsa_dtype;
+/* LVSA_FP32: fp32 in and out, fp32 products and accumulation (the reference
+ * computes in the caller's dtype, lvsa/sparse_attention.py:670, 689-704);
+ * 128-row tiles, text tiles unsplit.                                        */
+typedef enum lvsa_dtype { LVSA_BF16 = 0, LVSA_FP16 = 1, LVSA_FP32 = 2 } lvsa_dtype;
 
 /* ───────────────────────── frame mask builder ─────────────────────────── */
 
@@ -68,6 +71,15 @@ typedef struct lvsa_mask_params {
   int32_t rank;         /* context-parallel position; (0, 1) on one GPU         */
   int32_t world;
   uint32_t guard_bits[LVSA_BITMAP_WORDS]; /* boundary-guard frames, bit f = frame f */
+  /* Device re-tune (set_window_size / set_sparsity_scale,
+   * lvsa/lvsa_processor.py:288-315, 333-360): with auto_kfi = 1 the builder
+   * derives kfi from (T, window, n_first, reference_frames, sparsity_scale)
+   * as lvsa_auto_kfi does and uses offset = step % kfi; the kfi and offset
+   * fields are then ignored.  info[7] reports the kfi used either way.      */
+  int32_t auto_kfi;
+  int32_t reference_frames;  /* reference default 21                         */
+  double sparsity_scale;     /* reference default 1.0                        */
+  int64_t step;              /* denoising step index (>= 0)                  */
 } lvsa_mask_params;
 
 /* Output sizes of lvsa_mask_build (all int32 unless noted):
@@ -93,7 +105,8 @@ LVSA_API int lvsa_mask_sizes_query(const lvsa_mask_params* p, lvsa_mask_sizes* o
  *                                    bit g = frame g attended (globals + window)
  *   rel_window     [n_local*words]   uint32 bitmap of window_ctx frames only
  *   info           [8]               nnz, compact_n, n_global, n_rows,
- *                                    n_local, first_frame, max_row_nnz, 0      */
+ *                                    n_local, first_frame, max_row_nnz,
+ *                                    kfi used (0 = none)                      */
 typedef struct lvsa_mask_out {
   int32_t* frame_indptr;
   int32_t* frame_indices;
@@ -109,6 +122,14 @@ typedef struct lvsa_mask_out {
  * (lvsa/sparse_attention.py:89-104, 198-216, 550-635) as called from
  * LVSAMetadata.build (:335-484).  One work-group; enqueue only.              */
 LVSA_API int lvsa_mask_build(const lvsa_mask_params* p, const lvsa_mask_out* out, hipStream_t stream);
+
+/* compute_auto_kfi (lvsa/sparse_attention.py:132-195) on the device:
+ * *kfi_out (device int32) = the keyframe interval that gives about
+ * int(reference_frames * sparsity_scale) attended frames per query frame for
+ * T frames, window W and n_first anchors.  Used by the processor's re-tune
+ * (lvsa/lvsa_processor.py:303-309, 348-354).  One work-group; enqueue only. */
+LVSA_API int lvsa_auto_kfi(int32_t T, int32_t window, int32_t n_first, int32_t reference_frames,
+                           double sparsity_scale, int32_t* kfi_out, hipStream_t stream);
 
 /* ─────────────────────── block plan (token refinement) ──────────────────── */
 

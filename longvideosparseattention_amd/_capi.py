@@ -17,7 +17,7 @@ LIB_PATH = _PKG / "_lib" / "liblvsa_amd.so"
 
 LVSA_MAX_FRAMES = 4096
 LVSA_BITMAP_WORDS = LVSA_MAX_FRAMES // 32
-LVSA_BF16, LVSA_FP16 = 0, 1
+LVSA_BF16, LVSA_FP16, LVSA_FP32 = 0, 1, 2
 
 STATUS = {0: "ok", -1: "invalid argument", -2: "unsupported", -3: "capacity", -4: "hip error"}
 
@@ -42,6 +42,8 @@ class MaskParams(C.Structure):
         ("kfi", C.c_int32), ("offset", C.c_int32), ("expand", C.c_int32),
         ("rank", C.c_int32), ("world", C.c_int32),
         ("guard_bits", C.c_uint32 * LVSA_BITMAP_WORDS),
+        ("auto_kfi", C.c_int32), ("reference_frames", C.c_int32), ("sparsity_scale", C.c_double),
+        ("step", C.c_int64),
     ]
 
 
@@ -107,6 +109,8 @@ class AttnArgs(C.Structure):
 SIGNATURES = {
     "lvsa_mask_sizes_query": (C.c_int, [C.POINTER(MaskParams), C.POINTER(MaskSizes)]),
     "lvsa_mask_build": (C.c_int, [C.POINTER(MaskParams), C.POINTER(MaskOut), C.c_void_p]),
+    "lvsa_auto_kfi": (C.c_int, [C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_double, C.c_void_p,
+                                C.c_void_p]),
     "lvsa_plan_sizes_query": (C.c_int, [C.POINTER(PlanParams), C.c_int32, C.POINTER(PlanSizes)]),
     "lvsa_plan_build": (C.c_int, [C.POINTER(PlanParams), C.c_void_p, C.c_void_p, C.c_int64,
                                   C.c_void_p, C.c_int64, C.c_void_p]),

@@ -29,6 +29,13 @@ from .sparse_attention import LVSAMetadata, lvsa_sdpa
 _LN2 = math.log(2.0)
 
 
+def _torch_dtype(x: Any) -> Optional[torch.dtype]:
+    """FlashInfer's ``q_data_type`` (a torch dtype or its name) as a torch dtype."""
+    if isinstance(x, torch.dtype) or x is None:
+        return x
+    return getattr(torch, str(x).replace("torch.", ""), None)
+
+
 class BlockSparseAttentionWrapper:
     """HIP block-sparse attention over a block CSR (FlashInfer-compatible subset).
 
@@ -70,12 +77,22 @@ class BlockSparseAttentionWrapper:
         indices = indices.to(device)
         n_blocks_k = N // C
         self._bitmap, status = hip_ops.csr_to_bitmap(indptr, indices, n_blocks_k)
-        self._plan = hip_ops.plan_build(self._bitmap, n_q=M, n_k=N, R=R, Cf=C,
-                                        max_row_frames=max(1, n_blocks_k), head_dim=head_dim, device=device)
+        self._plans = {}
+        self._plan_args = dict(n_q=M, n_k=N, R=R, Cf=C, max_row_frames=max(1, n_blocks_k), device=device)
+        self._plan = self._plan_for(head_dim, _torch_dtype(q_data_type))
         self._shape = (M, N, num_qo_heads, num_kv_heads, head_dim)
         self._scale = sm_scale
         self._status = status
         self._status_checked = False
+
+    def _plan_for(self, head_dim: int, dtype: Optional[torch.dtype]) -> hip_ops.BlockPlan:
+        # one block plan per tile height: fp32 runs 128-row tiles
+        block_q = hip_ops.attn_block_q(head_dim, dtype)
+        plan = self._plans.get(block_q)
+        if plan is None:
+            plan = hip_ops.plan_build(self._bitmap, block_q=block_q, **self._plan_args)
+            self._plans[block_q] = plan
+        return plan
 
     def _check_columns(self) -> None:
         # status[0] of csr_to_bitmap flags column ids outside [0, N/C): such a
@@ -96,6 +113,7 @@ class BlockSparseAttentionWrapper:
         if q.shape != (M, H, D) or k.shape != (N, Hkv, D) or v.shape != (N, Hkv, D):
             raise ValueError(f"run() shapes {tuple(q.shape)}, {tuple(k.shape)} do not match the plan {self._shape}")
         self._check_columns()
+        self._plan = self._plan_for(D, q.dtype)
         o, _, lse_n, _ = hip_ops.attn_fwd(q.unsqueeze(0), k.unsqueeze(0), v.unsqueeze(0), self._plan,
                                           scale=self._scale, return_lse=return_lse)
         o = o[0]
@@ -120,11 +138,11 @@ def single_prefill_with_kv_cache(q: torch.Tensor, k: torch.Tensor, v: torch.Tens
     if causal:
         raise NotImplementedError("causal prefill is not part of the LVSA path")
     hip_ops._require_device(q, "q")
-    key = (q.device, q.shape[0], k.shape[0], hip_ops.attn_block_q(q.shape[-1]))
+    key = (q.device, q.shape[0], k.shape[0], hip_ops.attn_block_q(q.shape[-1], q.dtype))
     plan = _DENSE_PLANS.get(key)
     if plan is None:
         plan = hip_ops.plan_build(None, n_q=0, n_k=k.shape[0], n_tq=q.shape[0], head_dim=q.shape[-1],
-                                  device=q.device)
+                                  device=q.device, dtype=q.dtype)
         _DENSE_PLANS[key] = plan
     # Dense rows are the kernel's "text query" tiles: every key block, no mask.
     qt = q.unsqueeze(0)

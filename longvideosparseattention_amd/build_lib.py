@@ -37,6 +37,7 @@ SOURCES = {
     "lvsa_attn_d128.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"],
     "lvsa_attn_d192.hip": MAXOCC,
     "lvsa_attn_d256.hip": MAXOCC,
+    "lvsa_attn_f32.hip": [],
 }
 
 HIPCC_FLAGS = [

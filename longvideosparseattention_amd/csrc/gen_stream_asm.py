@@ -58,7 +58,7 @@ VM, VL, LS0, LS1, DMAROW, C16, DK, DV = 192, 193, 194, 195, 196, 197, 198, 199
 ROW, H4, NEGINF, VT, RT, T = 200, 201, 202, 203, 204, 208
 S_EPTR, S_N, S_CS = 20, 22, 23
 S_KB0, S_VB0, S_KB1, S_VB1 = 24, 26, 28, 30
-S_KRS0, S_VRS0, S_KRS1, S_VRS1, S_NK, S_NX, S_LDSK = 32, 33, 34, 35, 36, 37, 39
+S_KRS0, S_VRS0, S_KRS1, S_VRS1, S_NK, S_NX, S_WAVE, S_LDSK = 32, 33, 34, 35, 36, 37, 38, 39
 S_J, S_NM1, S_CUR, S_ENT, S_RK, S_RV = 40, 41, 42, 44, 52, 56
 S_SOK, S_SOV, S_KRSC = 60, 62, 64  # copy soffsets (K: 60, 61; V: 62, 63); strides, 32-row strides
 S_RET = 76

@@ -21,7 +21,7 @@ constexpr int kMaxTextChunks = 64;
 
 // Text chunks per text tile for the arguments (1 = no split).
 int text_chunks_of(const lvsa_attn_args* a) {
-  if (a->n_tq == 0) return 1;
+  if (a->n_tq == 0 || a->dtype == LVSA_FP32) return 1;   // the fp32 kernel runs text tiles whole
   const int64_t blocks = ceil_div(a->n_k, kBN) + ceil_div(a->n_x, kBN);
   const int64_t c = ceil_div(blocks, kTextChunkBlocks);
   return (int)(c < 1 ? 1 : (c > kMaxTextChunks ? kMaxTextChunks : c));
@@ -101,10 +101,10 @@ int scratch_of_current_device(void** out) {
   return LVSA_OK;
 }
 
-bool aligned16(const void* ptr, const int64_t* str, int n) {
+bool aligned16(const void* ptr, const int64_t* str, int n, int elem_bytes) {
   if (((uintptr_t)ptr) % 16) return false;
   for (int i = 0; i < n; ++i)
-    if ((str[i] * 2) % 16) return false;
+    if ((str[i] * elem_bytes) % 16) return false;
   return true;
 }
 
@@ -117,10 +117,14 @@ extern "C" int lvsa_attn_fwd(const lvsa_attn_args* a, hipStream_t stream) {
                "lvsa_attn_fwd: head_dim %d not supported (64, 96, 128, 192, 256)", a->D);
   LVSA_REQUIRE(a->D < 192 || a->block_q == kBM, LVSA_ERR_UNSUPPORTED,
                "lvsa_attn_fwd: head_dim %d runs 128-row tiles (block_q %d)", a->D, a->block_q);
-  LVSA_REQUIRE(a->D != 96 || a->block_q == kPPBM, LVSA_ERR_UNSUPPORTED,
+  LVSA_REQUIRE(a->dtype == LVSA_BF16 || a->dtype == LVSA_FP16 || a->dtype == LVSA_FP32, LVSA_ERR_UNSUPPORTED,
+               "lvsa_attn_fwd: dtype %d", a->dtype);
+  const bool fp32 = a->dtype == LVSA_FP32;
+  const int es = fp32 ? 4 : 2;   // bytes per element
+  LVSA_REQUIRE(fp32 || a->D != 96 || a->block_q == kPPBM, LVSA_ERR_UNSUPPORTED,
                "lvsa_attn_fwd: head_dim 96 runs 256-row tiles (block_q %d)", a->block_q);
-  LVSA_REQUIRE(a->dtype == LVSA_BF16 || a->dtype == LVSA_FP16, LVSA_ERR_UNSUPPORTED, "lvsa_attn_fwd: dtype %d",
-               a->dtype);
+  LVSA_REQUIRE(!fp32 || a->block_q == kBM, LVSA_ERR_UNSUPPORTED,
+               "lvsa_attn_fwd: fp32 runs 128-row tiles (block_q %d)", a->block_q);
   LVSA_REQUIRE(a->B >= 1 && a->H >= 1 && a->Hkv >= 1 && a->H % a->Hkv == 0, LVSA_ERR_INVALID_ARG,
                "lvsa_attn_fwd: B=%d H=%d Hkv=%d (H must be a multiple of Hkv)", a->B, a->H, a->Hkv);
   LVSA_REQUIRE(a->n_q >= 0 && a->n_k >= 0 && a->n_x >= 0 && a->n_tq >= 0, LVSA_ERR_INVALID_ARG,
@@ -138,13 +142,13 @@ extern "C" int lvsa_attn_fwd(const lvsa_attn_args* a, hipStream_t stream) {
   LVSA_REQUIRE(a->n_x == 0 || (a->kx && a->vx), LVSA_ERR_INVALID_ARG, "lvsa_attn_fwd: null extra k/v");
   LVSA_REQUIRE(a->n_k + a->n_x > 0 || a->n_tiles == 0, LVSA_ERR_INVALID_ARG, "lvsa_attn_fwd: no keys");
   bool ok = true;
-  if (a->n_q) ok = ok && aligned16(a->q, a->q_str, 3) && aligned16(a->o, a->o_str, 3);
-  if (a->n_tq) ok = ok && aligned16(a->qt, a->qt_str, 3) && aligned16(a->ot, a->ot_str, 3);
-  if (a->n_k) ok = ok && aligned16(a->k, a->k_str, 3) && aligned16(a->v, a->v_str, 3);
-  if (a->n_x) ok = ok && aligned16(a->kx, a->kx_str, 3) && aligned16(a->vx, a->vx_str, 3);
+  if (a->n_q) ok = ok && aligned16(a->q, a->q_str, 3, es) && aligned16(a->o, a->o_str, 3, es);
+  if (a->n_tq) ok = ok && aligned16(a->qt, a->qt_str, 3, es) && aligned16(a->ot, a->ot_str, 3, es);
+  if (a->n_k) ok = ok && aligned16(a->k, a->k_str, 3, es) && aligned16(a->v, a->v_str, 3, es);
+  if (a->n_x) ok = ok && aligned16(a->kx, a->kx_str, 3, es) && aligned16(a->vx, a->vx_str, 3, es);
   LVSA_REQUIRE(ok, LVSA_ERR_UNSUPPORTED, "lvsa_attn_fwd: tensors must be 16-byte aligned with 16-byte row strides");
   // per-lane DMA offsets within a 64-row key block are 32-bit
-  auto fits = [&](int64_t row_elems) { return row_elems >= 0 && row_elems * 2 * (kBN - 1) + 2LL * a->D <= 0xFFFFFFFFLL; };
+  auto fits = [&](int64_t row_elems) { return row_elems >= 0 && row_elems * es * (kBN - 1) + es * (int64_t)a->D <= 0xFFFFFFFFLL; };
   LVSA_REQUIRE(fits(a->k_str[1]) && fits(a->v_str[1]) && (a->n_x == 0 || (fits(a->kx_str[1]) && fits(a->vx_str[1]))),
                LVSA_ERR_UNSUPPORTED, "lvsa_attn_fwd: key/value row stride too large");
   // the 256-row kernel forms per-lane row offsets with 24-bit multiplies
@@ -233,12 +237,13 @@ extern "C" int lvsa_attn_fwd(const lvsa_attn_args* a, hipStream_t stream) {
   auto fits32 = [](int64_t rows, int64_t row_elems) { return (rows + kBN) * row_elems * 2 < (1LL << 32); };
   const bool src32 = fits32(a->n_k, a->k_str[1]) && fits32(a->n_k, a->v_str[1]) &&
                      (a->n_x == 0 || (fits32(a->n_x, a->kx_str[1]) && fits32(a->n_x, a->vx_str[1])));
-  p.use_stream = (a->D == 128 && a->block_q == kPPBM && !force_pp && src32 &&
+  p.use_stream = (!fp32 && a->D == 128 && a->block_q == kPPBM && !force_pp && src32 &&
                   (a->n_q == 0 || (p.R >= 255 && p.C >= 64))) ? 1 : 0;
   const int bq = a->block_q;
   const bool bf16 = a->dtype == LVSA_BF16;
   int rc;
-  if (a->D == 256) rc = launch_d256(p, bq, bf16, stream);
+  if (fp32) rc = launch_f32(p, a->D, stream);
+  else if (a->D == 256) rc = launch_d256(p, bq, bf16, stream);
   else if (a->D == 128) rc = launch_d128(p, bq, bf16, stream);
   else if (a->D == 96) rc = launch_d96(p, bq, bf16, stream);
   else if (a->D == 192) rc = launch_d192(p, bq, bf16, stream);

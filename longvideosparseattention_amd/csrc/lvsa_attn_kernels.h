@@ -89,6 +89,8 @@ int launch_d96(const AttnParams& prm, int block_q, bool bf16, hipStream_t stream
 int launch_d128(const AttnParams& prm, int block_q, bool bf16, hipStream_t stream);
 int launch_d192(const AttnParams& prm, int block_q, bool bf16, hipStream_t stream);
 int launch_d256(const AttnParams& prm, int block_q, bool bf16, hipStream_t stream);
+// fp32 inputs (lvsa_attn_f32.hip): 128-row tiles, every head size.
+int launch_f32(const AttnParams& prm, int D, hipStream_t stream);
 
 namespace {
 
@@ -296,6 +298,45 @@ __device__ __forceinline__ void item_entries(const AttnParams& p, const WorkItem
     e0 = a < e1 ? a : e1;
     e1 = e0 + len < e1 ? e0 + len : e1;
   }
+}
+
+// Mask of one key block for this lane's query row (row `tile_row` of its
+// tile, `my_row` of its source), for a block of kind two-part or generic:
+// bit r covers register r%16 of the S^T accumulator of key half r/16, which
+// holds key 8q + j + 4h of the block with q = r/4, j = r%4 (h = lane / 32).
+__device__ __forceinline__ uint32_t block_keep_bits(const AttnParams& p, uint32_t cx, uint32_t cy, int tile_row,
+                                                    int64_t my_row, int nrows, int h) {
+  if ((cy & 3u) == kKindTwoPart) {
+    const int bits = (cy >> 2) & 0xF;
+    const int kb = (int)((cy >> 8) & 0xFF) - 4 * h;
+    const int qs = (cy >> 16) & 0xFF;
+    const bool rb = tile_row >= qs;
+    const uint32_t lo_ok = (bits >> (rb ? 2 : 0)) & 1;
+    const uint32_t hi_ok = (bits >> (rb ? 3 : 1)) & 1;
+    int n_lo = 0;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int c = kb - 8 * q;
+      n_lo += c < 0 ? 0 : (c > 4 ? 4 : c);
+    }
+    const uint32_t lo_mask = n_lo >= 32 ? 0xFFFFFFFFu : ((1u << n_lo) - 1u);
+    return (lo_ok ? lo_mask : 0u) | (hi_ok ? ~lo_mask : 0u);
+  }
+  const bool extra = (cx >> 31) != 0;
+  const int64_t k0 = (int64_t)(cx & 0x7fffffffu) * kBN;
+  const int64_t nsrc = extra ? p.n_x : p.n_k;
+  const int64_t qtok = p.q_tok0 + (my_row < nrows ? my_row : (int64_t)nrows - 1);
+  const int qf_row = (int)(qtok / p.R) - p.q_frame0;
+  const uint32_t* relrow = p.rel + (int64_t)qf_row * p.words;
+  uint32_t keep = 0;
+  for (int r = 0; r < 32; ++r) {
+    const int64_t key = k0 + 8 * (r >> 2) + 4 * h + (r & 3);
+    if (key < nsrc) {
+      const int64_t kf = (p.k_tok0 + key) / p.C;
+      if ((kf >> 5) < p.words && ((relrow[kf >> 5] >> (kf & 31)) & 1u)) keep |= 1u << r;
+    }
+  }
+  return keep;
 }
 
 template <int D, typename E>
@@ -518,42 +559,10 @@ __global__ __launch_bounds__(kThreads, D >= 192 ? 1 : 2) void attn_fwd_kernel(At
       s1 = O::mfma(a1, qf[c], s1);
     }
 
-    // Masks.  Bit r of `keep` covers register r%16 of key half r/16, which
-    // holds key 8q + j + 4h of the block with q = r/4, j = r%4.
+    // Masks (bit r of `keep`: register r%16 of key half r/16).
     const uint32_t kind = cy & 3u;
     if (kind != kKindNone) {
-      uint32_t keep;
-      if (kind == kKindTwoPart) {
-        const int bits = (cy >> 2) & 0xF;
-        const int kb = (int)((cy >> 8) & 0xFF) - 4 * h;
-        const int qs = (cy >> 16) & 0xFF;
-        const bool rb = my_tile_row >= qs;
-        const uint32_t lo_ok = (bits >> (rb ? 2 : 0)) & 1;
-        const uint32_t hi_ok = (bits >> (rb ? 3 : 1)) & 1;
-        int n_lo = 0;
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          const int c = kb - 8 * q;
-          n_lo += c < 0 ? 0 : (c > 4 ? 4 : c);
-        }
-        const uint32_t lo_mask = n_lo >= 32 ? 0xFFFFFFFFu : ((1u << n_lo) - 1u);
-        keep = (lo_ok ? lo_mask : 0u) | (hi_ok ? ~lo_mask : 0u);
-      } else {
-        const bool extra = (cx >> 31) != 0;
-        const int64_t k0 = (int64_t)(cx & 0x7fffffffu) * kBN;
-        const int64_t nsrc = extra ? p.n_x : p.n_k;
-        const int64_t qtok = p.q_tok0 + (my_row < nrows ? my_row : (int64_t)nrows - 1);
-        const int qf_row = (int)(qtok / p.R) - p.q_frame0;
-        const uint32_t* relrow = p.rel + (int64_t)qf_row * p.words;
-        keep = 0;
-        for (int r = 0; r < 32; ++r) {
-          const int64_t key = k0 + 8 * (r >> 2) + 4 * h + (r & 3);
-          if (key < nsrc) {
-            const int64_t kf = (p.k_tok0 + key) / p.C;
-            if ((kf >> 5) < p.words && ((relrow[kf >> 5] >> (kf & 31)) & 1u)) keep |= 1u << r;
-          }
-        }
-      }
+      const uint32_t keep = block_keep_bits(p, cx, cy, my_tile_row, my_row, nrows, h);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         s0[r] = ((keep >> r) & 1u) ? s0[r] : -INFINITY;
@@ -1032,42 +1041,10 @@ __global__ __launch_bounds__(kPPThreads, 1) void attn_fwd_pp_kernel(AttnParams p
     advance(e0 + j);
     uint32_t cx, cy;
     entry(e0 + j, cx, cy);
-    // Bit r of `keep` covers register r%16 of key half r/16, which holds key
-    // 8q + jj + 4h of the block with q = r/4, jj = r%4.
+    // Masks (bit r of `keep`: register r%16 of key half r/16).
     const uint32_t kind = cy & 3u;
     if (kind != kKindNone) {
-      uint32_t keep;
-      if (kind == kKindTwoPart) {
-        const int bits = (cy >> 2) & 0xF;
-        const int kb = (int)((cy >> 8) & 0xFF) - 4 * h;
-        const int qs = (cy >> 16) & 0xFF;
-        const bool rb = my_tile_row >= qs;
-        const uint32_t lo_ok = (bits >> (rb ? 2 : 0)) & 1;
-        const uint32_t hi_ok = (bits >> (rb ? 3 : 1)) & 1;
-        int n_lo = 0;
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          const int c = kb - 8 * q;
-          n_lo += c < 0 ? 0 : (c > 4 ? 4 : c);
-        }
-        const uint32_t lo_mask = n_lo >= 32 ? 0xFFFFFFFFu : ((1u << n_lo) - 1u);
-        keep = (lo_ok ? lo_mask : 0u) | (hi_ok ? ~lo_mask : 0u);
-      } else {
-        const bool extra = (cx >> 31) != 0;
-        const int64_t k0 = (int64_t)(cx & 0x7fffffffu) * kBN;
-        const int64_t nsrc = extra ? p.n_x : p.n_k;
-        const int64_t qtok = p.q_tok0 + (my_row < nrows ? my_row : (int64_t)nrows - 1);
-        const int qf_row = (int)(qtok / p.R) - p.q_frame0;
-        const uint32_t* relrow = p.rel + (int64_t)qf_row * p.words;
-        keep = 0;
-        for (int r = 0; r < 32; ++r) {
-          const int64_t key = k0 + 8 * (r >> 2) + 4 * h + (r & 3);
-          if (key < nsrc) {
-            const int64_t kf = (p.k_tok0 + key) / p.C;
-            if ((kf >> 5) < p.words && ((relrow[kf >> 5] >> (kf & 31)) & 1u)) keep |= 1u << r;
-          }
-        }
-      }
+      const uint32_t keep = block_keep_bits(p, cx, cy, my_tile_row, my_row, nrows, h);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         s0[r] = ((keep >> r) & 1u) ? s0[r] : -INFINITY;

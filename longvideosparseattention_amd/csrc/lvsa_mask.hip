@@ -97,8 +97,50 @@ __device__ void frame_window(int f, int W, int T, bool expand, const uint8_t* gf
   *hi_out = (int)hi;
 }
 
+// compute_auto_kfi (lvsa/sparse_attention.py:132-195), evaluated by one
+// work-group.  Budget B = max(n + 1, int(ref * scale)); T <= B gives 1.
+// Otherwise the strict interval is the largest k in [1, T] whose grid
+// {0, k, 2k, ...} < T together with the anchors 0..a-1 (a = min(n, T)) holds
+// at least G = max(n, B - min(2W + 1, T)) frames, and that union has
+// a + ceil(T/k) - ceil(a/k) frames, so each thread tests its share of k in
+// O(1) each and the work-group takes the maximum.  The fallback is
+// ceil(max(T - M, B - M) / max(B - M, 1)) with M = 2W + n, the result the
+// larger of the two.  `budget` is int(ref * scale), truncated on the host.
+struct KfiArgs {
+  int T, window, n_first;
+  int64_t budget;
+};
+
+__device__ int auto_kfi_block(const KfiArgs& k, int* s_best) {
+  const int64_t T = k.T, n = k.n_first, W = k.window;
+  const int64_t B = max(n + 1, k.budget);
+  if (T <= B) return 1;                                   // uniform across the work-group
+  const int64_t G = max(n, B - min(2 * W + 1, T));
+  const int64_t a = max((int64_t)0, min(n, T));
+  if (threadIdx.x == 0) *s_best = 1;
+  __syncthreads();
+  int best = 0;
+  for (int64_t kk = threadIdx.x + 1; kk <= T; kk += blockDim.x) {
+    const int64_t u = a + ceil_div(T, kk) - ceil_div(a, kk);
+    if (u >= G) best = (int)kk;                           // ascending: the last hit is the largest
+  }
+  if (best) atomicMax(s_best, best);
+  __syncthreads();
+  const int strict = *s_best;
+  const int64_t M = 2 * W + n;
+  const int64_t num = max(T - M, B - M), den = max(B - M, (int64_t)1);
+  const int64_t fallback = num >= 0 ? (num + den - 1) / den : num / den;   // ceil; C division truncates
+  return (int)max((int64_t)strict, fallback);
+}
+
+__global__ __launch_bounds__(256) void auto_kfi_kernel(KfiArgs k, int32_t* out) {
+  __shared__ int s_best;
+  const int kfi = auto_kfi_block(k, &s_best);
+  if (threadIdx.x == 0) *out = kfi;
+}
+
 struct MaskGeom {
-  int64_t local, gts;
+  int64_t local, gts, budget;
   int T, P, first, n_local, n_rows, words;
 };
 
@@ -136,8 +178,16 @@ __global__ __launch_bounds__(kMaskThreads) void mask_build_kernel(lvsa_mask_para
   __shared__ int uprefix[LVSA_BITMAP_WORDS + 1];
   __shared__ int scan_sh[kMaskThreads];
   __shared__ int s_rowmax;
+  __shared__ int s_kfi;
 
   const int T = g.T, tid = threadIdx.x, nt = blockDim.x;
+
+  // 0. keyframe interval and offset: given, or derived here (device re-tune).
+  int kfi = p.kfi, offset = p.offset;
+  if (p.auto_kfi) {
+    kfi = auto_kfi_block(KfiArgs{T, p.window, p.n_first, g.budget}, &s_kfi);
+    offset = (int)(p.step % kfi);
+  }
 
   // 1. global flags: anchors, boundary guards, rotated keyframe grid (mod T).
   for (int i = tid; i < T; i += nt)
@@ -145,10 +195,10 @@ __global__ __launch_bounds__(kMaskThreads) void mask_build_kernel(lvsa_mask_para
   for (int w = tid; w < LVSA_BITMAP_WORDS; w += nt) uni[w] = 0;
   if (tid == 0) s_rowmax = 0;
   __syncthreads();
-  if (p.kfi > 0) {
-    const int nkey = (T + p.kfi - 1) / p.kfi;
+  if (kfi > 0) {
+    const int nkey = (T + kfi - 1) / kfi;
     for (int i = tid; i < nkey; i += nt) {
-      int64_t x = ((int64_t)p.offset + (int64_t)i * p.kfi) % T;
+      int64_t x = ((int64_t)offset + (int64_t)i * kfi) % T;
       if (x < 0) x += T;
       gflag[x] = 1;
     }
@@ -259,7 +309,7 @@ __global__ __launch_bounds__(kMaskThreads) void mask_build_kernel(lvsa_mask_para
     out.info[4] = g.n_local;
     out.info[5] = g.first;
     out.info[6] = s_rowmax;
-    out.info[7] = 0;
+    out.info[7] = kfi > 0 ? kfi : 0;
   }
 }
 
@@ -445,8 +495,19 @@ const char* lvsa_version(void) { return LVSA_AMD_VERSION; }
 
 const char* lvsa_last_error(void) { return g_last_error.c_str(); }
 
+// int(reference_frames * sparsity_scale) as Python computes it (a double
+// product truncated toward zero); NaN is an error there too.
+static int kfi_budget(int32_t reference_frames, double sparsity_scale, int64_t* budget) {
+  const double prod = (double)reference_frames * sparsity_scale;
+  LVSA_REQUIRE(prod == prod, LVSA_ERR_INVALID_ARG, "lvsa: sparsity_scale is NaN");
+  *budget = prod >= 9.0e18 ? INT64_MAX : prod <= -9.0e18 ? INT64_MIN : (int64_t)prod;
+  return LVSA_OK;
+}
+
 static int mask_geometry(const lvsa_mask_params* p, lvsa_mask_sizes* s, MaskGeom* g) {
   LVSA_REQUIRE(p != nullptr, LVSA_ERR_INVALID_ARG, "lvsa_mask: null params");
+  int rc = LVSA_OK;
+  int64_t budget = 0;
   LVSA_REQUIRE(p->T >= 1 && p->T <= LVSA_MAX_FRAMES, LVSA_ERR_INVALID_ARG,
                "lvsa_mask: T=%d outside [1, %d]", p->T, LVSA_MAX_FRAMES);
   LVSA_REQUIRE(p->P >= 1, LVSA_ERR_INVALID_ARG, "lvsa_mask: P=%d must be >= 1", p->P);
@@ -459,6 +520,11 @@ static int mask_geometry(const lvsa_mask_params* p, lvsa_mask_sizes* s, MaskGeom
   LVSA_REQUIRE(total % p->world == 0, LVSA_ERR_INVALID_ARG,
                "total_seq=%lld (T=%d x P=%d) must be divisible by world=%d.", (long long)total, p->T, p->P,
                p->world);
+  if (p->auto_kfi) {
+    LVSA_REQUIRE(p->step >= 0, LVSA_ERR_INVALID_ARG, "lvsa_mask: step=%lld must be >= 0", (long long)p->step);
+    rc = kfi_budget(p->reference_frames, p->sparsity_scale, &budget);
+    if (rc) return rc;
+  }
   const int64_t local = total / p->world, gts = (int64_t)p->rank * local;
   const int first = (int)(gts / p->P), last = (int)((gts + local - 1) / p->P);
   s->local_seq = local;
@@ -470,6 +536,7 @@ static int mask_geometry(const lvsa_mask_params* p, lvsa_mask_sizes* s, MaskGeom
   if (g) {
     g->local = local;
     g->gts = gts;
+    g->budget = budget;
     g->T = p->T;
     g->P = p->P;
     g->first = first;
@@ -497,6 +564,21 @@ int lvsa_mask_build(const lvsa_mask_params* p, const lvsa_mask_out* out, hipStre
                LVSA_ERR_INVALID_ARG, "lvsa_mask_build: null output pointer");
   hipLaunchKernelGGL(mask_build_kernel, dim3(1), dim3(kMaskThreads), 0, stream, *p, g, *out);
   return launch_status("lvsa_mask_build");
+}
+
+int lvsa_auto_kfi(int32_t T, int32_t window, int32_t n_first, int32_t reference_frames, double sparsity_scale,
+                  int32_t* kfi_out, hipStream_t stream) {
+  clear_error();
+  LVSA_REQUIRE(T >= 1, LVSA_ERR_INVALID_ARG, "lvsa_auto_kfi: T=%d must be >= 1", T);
+  LVSA_REQUIRE(window >= 0 && window <= 1 << 28, LVSA_ERR_INVALID_ARG, "lvsa_auto_kfi: window=%d out of range",
+               window);
+  LVSA_REQUIRE(n_first >= 0, LVSA_ERR_INVALID_ARG, "lvsa_auto_kfi: n_first=%d must be >= 0", n_first);
+  LVSA_REQUIRE(kfi_out != nullptr, LVSA_ERR_INVALID_ARG, "lvsa_auto_kfi: null output");
+  int64_t budget;
+  const int rc = kfi_budget(reference_frames, sparsity_scale, &budget);
+  if (rc) return rc;
+  hipLaunchKernelGGL(auto_kfi_kernel, dim3(1), dim3(256), 0, stream, KfiArgs{T, window, n_first, budget}, kfi_out);
+  return launch_status("lvsa_auto_kfi");
 }
 
 static int plan_ctx(const lvsa_plan_params* p, PlanCtx* c) {

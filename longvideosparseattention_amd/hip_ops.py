@@ -17,7 +17,7 @@ import torch
 
 from . import _capi as capi
 
-_DTYPES = {torch.bfloat16: capi.LVSA_BF16, torch.float16: capi.LVSA_FP16}
+_DTYPES = {torch.bfloat16: capi.LVSA_BF16, torch.float16: capi.LVSA_FP16, torch.float32: capi.LVSA_FP32}
 # Head sizes of the reference plugin (LVSABackend.get_supported_head_sizes,
 # backend.py:52-53), all run natively: 96 on the 128 LDS layout, 192 on the
 # 256 one.
@@ -29,15 +29,17 @@ def kernel_head_dim(head_dim: int) -> int:
     return head_dim
 
 
-def attn_block_q(head_dim: int = 128) -> int:
+def attn_block_q(head_dim: int = 128, dtype: Optional[torch.dtype] = None) -> int:
     """Query rows per attention tile, i.e. which kernel a plan is built for.
 
-    256 for head sizes 64, 96 and 128: the 8-wave kernel whose two wave
-    groups alternate MFMA and softmax phases.  128 for 192 and 256: the
-    4-wave kernel (the 8-wave kernel's registers hold no Q and O that wide).
-    ``LVSA_ATTN_BLOCK_Q`` (128 or 256) overrides the choice for 64 and 128;
-    96 runs on the 8-wave kernel only."""
+    256 for head sizes 64, 96 and 128: the 8-wave kernels (bf16 / fp16).
+    128 for 192 and 256: the 4-wave kernel (the 8-wave kernels' registers
+    hold no Q and O that wide), and for fp32 inputs at every head size (the
+    fp32 kernel).  ``LVSA_ATTN_BLOCK_Q`` (128 or 256) overrides the choice for
+    64 and 128 in 16-bit; 96 runs on the 8-wave kernel only."""
     kd = kernel_head_dim(head_dim)
+    if dtype == torch.float32:
+        return 128
     if kd >= 192:
         return 128
     if kd == 96:
@@ -88,7 +90,12 @@ class DeviceMask:
 
 def mask_params(T: int, P: int, W: int, n_first: int, kfi: Optional[int], offset: int = 0,
                 expand: bool = True, rank: int = 0, world: int = 1,
-                guards: Sequence[int] = ()) -> capi.MaskParams:
+                guards: Sequence[int] = (), auto_step: Optional[int] = None,
+                reference_frames: int = 21, sparsity_scale: float = 1.0) -> capi.MaskParams:
+    """Parameters of ``lvsa_mask_build``.  With ``auto_step`` set, the kernel
+    derives kfi itself (``compute_auto_kfi`` of the window, ``reference_frames``
+    and ``sparsity_scale``) and rotates by ``auto_step % kfi``; ``kfi`` and
+    ``offset`` are then ignored."""
     if not 1 <= T <= capi.LVSA_MAX_FRAMES:
         raise ValueError(f"total_latent_frames={T} outside [1, {capi.LVSA_MAX_FRAMES}]")
     p = capi.MaskParams()
@@ -98,7 +105,27 @@ def mask_params(T: int, P: int, W: int, n_first: int, kfi: Optional[int], offset
     for g in guards:
         if 0 <= g < T:
             p.guard_bits[g >> 5] |= 1 << (g & 31)
+    p.reference_frames, p.sparsity_scale = int(reference_frames), float(sparsity_scale)
+    if auto_step is not None:
+        p.auto_kfi, p.step = 1, int(auto_step)
     return p
+
+
+def auto_kfi(T: int, W: int, n_first: int, reference_frames: int = 21, sparsity_scale: float = 1.0,
+             device: Optional[torch.device] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``compute_auto_kfi`` on the GPU (``lvsa_auto_kfi``): a one-element
+    int32 device tensor, written on the current stream."""
+    if out is None:
+        device = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+        if device.type != "cuda":
+            raise RuntimeError("lvsa_auto_kfi runs on the GPU only")
+        out = torch.empty(1, dtype=torch.int32, device=device)
+    _require_device(out, "kfi output")
+    with torch.cuda.device(out.device):
+        capi.check("lvsa_auto_kfi", capi.lib().lvsa_auto_kfi(
+            int(T), int(W), int(n_first), int(reference_frames), float(sparsity_scale), out.data_ptr(),
+            _stream(out.device)))
+    return out
 
 
 def mask_sizes(p: capi.MaskParams) -> capi.MaskSizes:
@@ -180,11 +207,12 @@ class BlockPlan:
 def plan_build(rel: Optional[torch.Tensor], *, n_q: int, n_k: int, n_x: int = 0, n_tq: int = 0,
                R: int = 1, Cf: int = 1, q_tok0: int = 0, k_tok0: int = 0, q_frame0: int = 0,
                max_row_frames: int = 0, block_q: Optional[int] = None, block_k: int = capi.ATTN_BLOCK_K,
-               head_dim: int = 128, device: Optional[torch.device] = None) -> BlockPlan:
+               head_dim: int = 128, device: Optional[torch.device] = None,
+               dtype: Optional[torch.dtype] = None) -> BlockPlan:
     """Refine a frame relation (bitmap rows x words, int32) to token blocks.
 
     ``block_q`` defaults to the tile height of the kernel that serves
-    ``head_dim`` (see :func:`attn_block_q`)."""
+    ``head_dim`` and ``dtype`` (see :func:`attn_block_q`)."""
     if rel is not None:
         _require_device(rel, "relation bitmap")
         device = rel.device
@@ -193,7 +221,7 @@ def plan_build(rel: Optional[torch.Tensor], *, n_q: int, n_k: int, n_x: int = 0,
         raise RuntimeError("lvsa_plan_build runs on the GPU only")
     device = torch.device(device)
     if block_q is None:
-        block_q = attn_block_q(head_dim)
+        block_q = attn_block_q(head_dim, dtype)
     p = capi.PlanParams()
     p.n_q, p.n_k, p.n_x, p.n_tq = n_q, n_k, n_x, n_tq
     p.R, p.C = R, Cf
@@ -255,7 +283,7 @@ def attn_args(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, plan: BlockPlan
     """Validate an attention call and fill its ``lvsa_attn_args`` (no workspace)."""
     dtype = q.dtype
     if dtype not in _DTYPES:
-        raise TypeError(f"unsupported dtype {dtype}: bf16 or fp16 inputs (fp32 callers cast first)")
+        raise TypeError(f"unsupported dtype {dtype}: bf16, fp16 or fp32 inputs")
     q = _prep(q, "query", dtype)
     k = _prep(k, "key", dtype)
     v = _prep(v, "value", dtype)

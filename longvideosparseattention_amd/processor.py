@@ -34,6 +34,7 @@ from . import hip_ops
 from .global_kv import build_global_kv
 from .sparse_attention import (
     LVSAMetadata,
+    _compute_dtype,
     adaptive_window_bounds,
     compute_auto_kfi,
     compute_boundary_guard_frames,
@@ -175,10 +176,21 @@ class DistributedLVSAProcessor:
             return
         self._rebuild_for_current_params(offset)
 
-    def _retune_kfi(self) -> None:
-        self.key_frame_interval = compute_auto_kfi(
+    def _derive_kfi(self) -> int:
+        """``compute_auto_kfi`` for the current window and budget.  With a GPU
+        present it runs as ``lvsa_auto_kfi`` on the device (one 4-byte read
+        back, since the host pattern fields depend on it); host-only processes
+        (no HIP device) evaluate the reference's formula in Python."""
+        if torch.cuda.is_available():
+            kfi = hip_ops.auto_kfi(self.total_num_frames, self.window_size, self.n_first_frames,
+                                   self._reference_frames, self._sparsity_scale)
+            return int(kfi.item())
+        return compute_auto_kfi(
             self.total_num_frames, self.window_size, self.n_first_frames,
             reference_frames=self._reference_frames, sparsity_scale=self._sparsity_scale)
+
+    def _retune_kfi(self) -> None:
+        self.key_frame_interval = self._derive_kfi()
         old_offset = self._current_offset
         self._current_offset = -1
         self._rebuild_for_current_params(old_offset)
@@ -252,13 +264,13 @@ class DistributedLVSAProcessor:
         L, S = query.shape[1], key.shape[1]
         n_x = 0 if enc_k is None else enc_k.shape[1]
         qt = query if enc_q is None else torch.cat([query, enc_q], 1)
-        pkey = (query.device, qt.shape[1], S, n_x, query.shape[-1])
+        dt = _compute_dtype(query)
+        pkey = (query.device, qt.shape[1], S, n_x, query.shape[-1], dt)
         plan = self._dense_plans.get(pkey)
         if plan is None:
             plan = hip_ops.plan_build(None, n_q=0, n_k=S, n_x=n_x, n_tq=qt.shape[1], head_dim=query.shape[-1],
-                                      device=query.device)
+                                      device=query.device, dtype=dt)
             self._dense_plans[pkey] = plan
-        dt = query.dtype if query.dtype in (torch.bfloat16, torch.float16) else torch.bfloat16
         cast = lambda x: None if x is None else x.to(dt)  # noqa: E731
         empty_q = qt.new_empty(qt.shape[0], 0, qt.shape[2], qt.shape[3], dtype=dt)
         _, o, _, _ = hip_ops.attn_fwd(empty_q, cast(key), cast(value), plan, kx=cast(enc_k), vx=cast(enc_v),

@@ -436,11 +436,11 @@ class LVSAMetadata:
     # ── Block plans (cached per device and call geometry) ──
 
     def window_plan(self, device: torch.device, n_q: int, n_k: int, n_extra: int,
-                    head_dim: int = 128) -> hip_ops.BlockPlan:
+                    head_dim: int = 128, dtype: Optional[torch.dtype] = None) -> hip_ops.BlockPlan:
         """Plan for ``lvsa_sdpa`` semantics: every query row attends all extra
         rows (``k_global``) plus the non-global window frames of its frame."""
         st = self.device_state(device)
-        block_q = hip_ops.attn_block_q(head_dim)
+        block_q = hip_ops.attn_block_q(head_dim, dtype)
         key = ("window", n_q, n_k, n_extra, block_q)
         plan = st.plans.get(key)
         if plan is None:
@@ -452,13 +452,13 @@ class LVSAMetadata:
         return plan
 
     def full_plan(self, device: torch.device, n_q: int, n_k: int, n_text_k: int, n_text_q: int,
-                  head_dim: int = 128) -> hip_ops.BlockPlan:
+                  head_dim: int = 128, dtype: Optional[torch.dtype] = None) -> hip_ops.BlockPlan:
         """Zero-copy plan: query rows attend their global + window frames of
         ``key`` directly, all text keys, and text queries attend everything."""
         if self.world != 1:
             raise NotImplementedError("zero-copy LVSA attention needs the whole sequence on one GPU (world=1)")
         st = self.device_state(device)
-        block_q = hip_ops.attn_block_q(head_dim)
+        block_q = hip_ops.attn_block_q(head_dim, dtype)
         key = ("full", n_q, n_k, n_text_k, n_text_q, block_q)
         plan = st.plans.get(key)
         if plan is None:
@@ -474,11 +474,14 @@ class LVSAMetadata:
 # Backends
 # ═══════════════════════════════════════════════════════════════════════════════
 
-_COMPUTE_DTYPES = (torch.bfloat16, torch.float16)
+_COMPUTE_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
 
 
 def _compute_dtype(t: torch.Tensor) -> torch.dtype:
-    return t.dtype if t.dtype in _COMPUTE_DTYPES else torch.bfloat16
+    """The caller's dtype, as the reference computes (``lvsa/sparse_attention.py:670,
+    689-704``): bf16 and fp16 on the 16-bit MFMA kernels, fp32 on the fp32
+    kernel; other types (fp64) run in fp32 and are cast back."""
+    return t.dtype if t.dtype in _COMPUTE_DTYPES else torch.float32
 
 
 def _check_local_seq(query: torch.Tensor, metadata: LVSAMetadata) -> None:
@@ -514,13 +517,14 @@ def lvsa_sdpa(
     query : [B, local_seq, H, D];  key, value, k_global, v_global : [B, *, H_kv, D]
         ``H_kv`` may divide ``H`` (grouped-query attention, handled natively).
     ``attention_backend`` is accepted for signature compatibility and ignored.
-    Returns a new tensor with the dtype of ``query`` (fp32 callers are
-    computed in bf16 and cast back).
+    Returns a new tensor with the dtype of ``query``, computed in that dtype
+    (fp64 in fp32).
     """
     _check_local_seq(query, metadata)
     hip_ops._require_device(query, "query")
     dt = _compute_dtype(query)
-    plan = metadata.window_plan(query.device, query.shape[1], key.shape[1], k_global.shape[1], query.shape[-1])
+    plan = metadata.window_plan(query.device, query.shape[1], key.shape[1], k_global.shape[1], query.shape[-1],
+                                dt)
     q, k, v, kg, vg = (x if x.dtype == dt else x.to(dt) for x in (query, key, value, k_global, v_global))
     out, _, _, _ = hip_ops.attn_fwd(q, k, v, plan, kx=kg, vx=vg)
     return out if out.dtype == query.dtype else out.to(query.dtype)
@@ -606,7 +610,7 @@ def lvsa_attention(
     dt = _compute_dtype(query)
     n_tk = 0 if k_text is None else k_text.shape[1]
     n_tq = 0 if q_text is None else q_text.shape[1]
-    plan = metadata.full_plan(query.device, query.shape[1], key.shape[1], n_tk, n_tq, query.shape[-1])
+    plan = metadata.full_plan(query.device, query.shape[1], key.shape[1], n_tk, n_tq, query.shape[-1], dt)
     cast = lambda x: x if (x is None or x.dtype == dt) else x.to(dt)  # noqa: E731
     out, out_t, lse, lse_t = hip_ops.attn_fwd(
         cast(query), cast(key), cast(value), plan, kx=cast(k_text), vx=cast(v_text), qt=cast(q_text),

@@ -234,6 +234,8 @@ class Wave:
             self.scc = int(self.sval(a[0]) == self.sval(a[1]))
         elif op == 's_cmp_lg_u32':
             self.scc = int(self.sval(a[0]) != self.sval(a[1]))
+        elif op == 's_cmp_lt_u32':
+            self.scc = int(self.sval(a[0]) < self.sval(a[1]))
         elif op == 's_cmp_ge_u32':
             self.scc = int(self.sval(a[0]) >= self.sval(a[1]))
         elif op == 's_bfe_u32':

@@ -76,6 +76,26 @@ def test_mask_sizes_and_errors():
     assert b"divisible by world" in lib.lvsa_last_error()
 
 
+def test_auto_kfi_rejects_bad_arguments_without_launching():
+    lib = _capi.lib()
+    assert lib.lvsa_auto_kfi(0, 2, 1, 21, 1.0, 8, None) == -1
+    assert b"T=0" in lib.lvsa_last_error()
+    assert lib.lvsa_auto_kfi(84, -1, 1, 21, 1.0, 8, None) == -1
+    assert lib.lvsa_auto_kfi(84, 2, 1, 21, 1.0, None, None) == -1
+    assert lib.lvsa_auto_kfi(84, 2, 1, 21, float("nan"), 8, None) == -1
+    assert b"NaN" in lib.lvsa_last_error()
+    # the mask builder's device re-tune checks the same budget on the host
+    p = _capi.MaskParams(T=84, P=1560, window=2, n_first=1, expand=1, rank=0, world=1, auto_kfi=1,
+                         reference_frames=21, sparsity_scale=float("nan"), step=3)
+    s = _capi.MaskSizes()
+    assert lib.lvsa_mask_sizes_query(C.byref(p), C.byref(s)) == -1
+    p.sparsity_scale, p.step = 0.5, -1
+    assert lib.lvsa_mask_sizes_query(C.byref(p), C.byref(s)) == -1
+    assert b"step=-1" in lib.lvsa_last_error()
+    p.step = 3
+    assert lib.lvsa_mask_sizes_query(C.byref(p), C.byref(s)) == 0
+
+
 def test_plan_sizes():
     lib = _capi.lib()
     p = _capi.PlanParams(n_q=131040, n_k=131040, n_x=0, n_tq=0, R=1560, C=1560, q_tok0=0, k_tok0=0,

@@ -271,9 +271,95 @@ def test_batch_views_and_fp32_inputs(gpu):
     for b in range(2):
         ro, _ = oa.per_frame_sdpa(q[b:b + 1].float(), k[b:b + 1].float(), v[b:b + 1].float(), rows, P)
         _close(out[b:b + 1], ro, f"batch {b}")
-    out32 = lv.lvsa_attention(q.float(), k.float(), v.float(), m)
+    out32 = lv.lvsa_attention(q.float(), k.float(), v.float(), m)   # fp32 kernel, strided fp32 copies
     assert out32.dtype == torch.float32
-    _close(out32, out.float(), "fp32 inputs", max_abs=1e-6, mean_abs=1e-7)
+    for b in range(2):
+        ro, _ = oa.per_frame_sdpa(q[b:b + 1].float(), k[b:b + 1].float(), v[b:b + 1].float(), rows, P)
+        _close(out32[b:b + 1], ro, f"fp32 batch {b}", max_abs=FP32_MAX_ABS, mean_abs=FP32_MEAN_ABS)
+
+
+# fp32 callers compute in fp32 (fp32 MFMA products and accumulation, exact
+# online softmax): tolerance against the fp32 oracle about 400x tighter
+# than the 16-bit path's.
+FP32_MAX_ABS = 5e-5
+FP32_MEAN_ABS = 5e-6
+
+
+def test_fp32_baseline_config_1(gpu):
+    """BASELINE config 1 (fp32, 12 heads, D 128, 9 frames x 256 tokens, 1
+    anchor, keyframe stride 4 rotated by step 3, window 1) through
+    lvsa_sdpa and lvsa_attention, against the fp32 oracle on the CPU."""
+    T, P, W, kfi, off, H, D = 9, 256, 1, 4, 3, 12, 128
+    N = T * P
+    q, k, v = _draw([(1, N, H, D)] * 3, dtype=torch.float32)
+    m = _meta(T, P, W, 1, kfi, off)
+    rows = [set(r) for r in om.build_frame_mask(T, P, W, 1, kfi, offset=off).rows]
+    ro, rl = oa.per_frame_sdpa(q, k, v, rows, P)
+    o, lse = lv.lvsa_attention(q.to(gpu), k.to(gpu), v.to(gpu), m, return_lse=True)
+    assert o.dtype == torch.float32
+    _close(o, ro, "fp32 lvsa_attention", max_abs=FP32_MAX_ABS, mean_abs=FP32_MEAN_ABS)
+    torch.testing.assert_close(lse.cpu(), rl, atol=2e-5, rtol=1e-6)
+    # the reference's lvsa_sdpa semantics: pre-gathered globals + window frames
+    kd, vd = k.to(gpu), v.to(gpu)
+    kg, vg = lv.build_global_kv(kd, vd, m.global_indices, P)
+    o2 = lv.lvsa_sdpa(q.to(gpu), kd, vd, kg, vg, m)
+    _close(o2, ro, "fp32 lvsa_sdpa", max_abs=FP32_MAX_ABS, mean_abs=FP32_MEAN_ABS)
+    # the bf16 path on the same data is within the 16-bit tolerance only
+    ob = lv.lvsa_attention(*(x.to(gpu, torch.bfloat16) for x in (q, k, v)), m)
+    assert (ob.float().cpu() - ro).abs().max().item() > 20 * FP32_MAX_ABS
+
+
+@pytest.mark.parametrize("cfg", SMALL, ids=[str(c[:10]) for c in SMALL])
+def test_fp32_small_configs(cfg, gpu):
+    """fp32 over the small grid: every head size, GQA, text keys and text
+    queries, W = 0 and frames below a tile (generic masks), kfi = 1."""
+    T, P, W, n, kfi, off, H, Hkv, D, n_txt, _ = cfg
+    N = T * P
+    q, k, v, qt, kt, vt = _draw([(1, N, H, D), (1, N, Hkv, D), (1, N, Hkv, D), (1, n_txt, H, D),
+                                 (1, n_txt, Hkv, D), (1, n_txt, Hkv, D)], seed=4, dtype=torch.float32)
+    m = _meta(T, P, W, n, kfi, off)
+    g = [x.to(gpu) for x in (q, k, v, qt, kt, vt)]
+    rows = [set(r) for r in om.build_frame_mask(T, P, W, n, kfi, offset=off).rows]
+    ro, rl = oa.per_frame_sdpa(q, k, v, rows, P, k_extra=kt if n_txt else None, v_extra=vt if n_txt else None)
+    if n_txt:
+        o, ot, lse, lse_t = lv.lvsa_attention(g[0], g[1], g[2], m, k_text=g[4], v_text=g[5], q_text=g[3],
+                                              return_lse=True)
+        rto, rtl = oa.text_row_attention(qt, k, v, kt, vt)
+        _close(ot, rto, "fp32 text rows", max_abs=FP32_MAX_ABS, mean_abs=FP32_MEAN_ABS)
+        torch.testing.assert_close(lse_t.cpu(), rtl, atol=2e-5, rtol=1e-6)
+    else:
+        o, lse = lv.lvsa_attention(g[0], g[1], g[2], m, return_lse=True)
+    _close(o, ro, f"fp32 D={D}", max_abs=FP32_MAX_ABS, mean_abs=FP32_MEAN_ABS)
+    torch.testing.assert_close(lse.cpu(), rl, atol=2e-5, rtol=1e-6)
+
+
+def test_fp32_wrapper_and_prefill(gpu):
+    """fp32 through the block-sparse wrapper (planned for fp16, run in fp32:
+    the wrapper re-plans for 128-row tiles) and the dense prefill."""
+    R, C, nb, H, D = 64, 64, 6, 2, 128
+    g = torch.Generator().manual_seed(9)
+    indptr = torch.tensor([0, 2, 3, 6, 6, 8, 9], dtype=torch.int32)
+    indices = torch.tensor([0, 3, 1, 5, 2, 0, 4, 1, 3], dtype=torch.int32)
+    q, k, v = (torch.randn(nb * R, H, D, generator=g) for _ in range(3))
+    w = lv.BlockSparseAttentionWrapper()
+    w.plan(indptr.to(gpu), indices.to(gpu), nb * R, nb * C, R, C, H, H, D)
+    o = w.run(q.to(gpu), k.to(gpu), v.to(gpu))
+    assert o.dtype == torch.float32
+    for i in range(nb):
+        cols = indices[indptr[i]:indptr[i + 1]].tolist()
+        rows = slice(i * R, (i + 1) * R)
+        if not cols:
+            assert (o[rows] == 0).all()
+            continue
+        kk = torch.cat([k[c * C:(c + 1) * C] for c in cols])
+        vv = torch.cat([v[c * C:(c + 1) * C] for c in cols])
+        ro, _ = oa.dense_attention(q[rows].unsqueeze(0), kk.unsqueeze(0), vv.unsqueeze(0))
+        _close(o[rows].unsqueeze(0), ro, f"fp32 wrapper row block {i}", max_abs=FP32_MAX_ABS,
+               mean_abs=FP32_MEAN_ABS)
+    qd, kd, vd = (torch.randn(*s, generator=g) for s in ((70, 4, 64), (3000, 2, 64), (3000, 2, 64)))
+    od = lv.single_prefill_with_kv_cache(qd.to(gpu), kd.to(gpu), vd.to(gpu))
+    rd, _ = oa.dense_attention(qd.unsqueeze(0), kd.unsqueeze(0), vd.unsqueeze(0))
+    _close(od.unsqueeze(0), rd, "fp32 prefill", max_abs=FP32_MAX_ABS, mean_abs=FP32_MEAN_ABS)
 
 
 EXTREME = ["hot", "cold", "cold_then_hot", "hot_then_cold"]
@@ -371,6 +457,57 @@ def test_baseline_config_parity(cfg, gpu):
         rto, _ = oa.text_row_attention(qt.to(gpu).float(), kd.float(), vd.float(), kt.to(gpu).float(),
                                        vt.to(gpu).float())
         _close(ot, rto, name + " text rows")
+
+
+SWEEP = [
+    # name, T, P, W, kfi, H, D, n_txt, offsets (full BASELINE sizes, bf16)
+    ("wan4x", 84, 1560, 2, 8, 12, 128, 0, tuple(range(8))),
+    ("hv", 49, 1590, 2, 8, 16, 128, 256, tuple(range(8))),
+    ("wan6x_w2", 121, 1560, 2, 8, 12, 128, 0, (0, 3, 6)),
+    ("wan6x_w4", 121, 1560, 4, 8, 12, 128, 0, (1, 7)),
+]
+
+
+def _sweep_frames(T, P, kfi, off):
+    """Query frames to compare: first / last, the rotated keyframes and their
+    neighbours (rows that gain or lose a global frame with the offset), and
+    the frames whose first row lies nearest above a 256-row tile edge and a
+    128-row block edge."""
+    fs = {0, 1, T - 1, off % T, (off + 1) % T, (off - 1) % T}
+    mid = off + kfi * ((T // kfi) // 2)
+    fs |= {mid % T, (mid + 1) % T}
+    fs.add(min(range(1, T), key=lambda f: (f * P) % 256))
+    fs.add(min(range(1, T), key=lambda f: (-(f * P)) % 128))
+    return sorted(fs)
+
+
+@pytest.mark.parametrize("cfg", SWEEP, ids=[c[0] for c in SWEEP])
+def test_baseline_sweep_spot_frames(cfg, gpu):
+    """Every keyframe rotation of Wan 4x and HunyuanVideo and the window
+    sweep of Wan 6x, at full size through lvsa_attention: about 9 query
+    frames per offset against the fp32 oracle, all frames by properties."""
+    name, T, P, W, kfi, H, D, n_txt, offsets = cfg
+    N = T * P
+    g = torch.Generator(device=gpu).manual_seed(11)
+    q, k, v = (torch.randn(1, N, H, D, generator=g, device=gpu).to(torch.bfloat16) for _ in range(3))
+    qt, kt, vt = (torch.randn(1, n_txt, H, D, generator=g, device=gpu).to(torch.bfloat16) for _ in range(3))
+    qf, kf, vf = q.float(), k.float(), v.float()
+    vmax = max(v.abs().max().item(), vt.abs().max().item() if n_txt else 0.0)
+    for off in offsets:
+        m = _meta(T, P, W, 1, kfi, off)
+        if n_txt:
+            o, ot = lv.lvsa_attention(q, k, v, m, k_text=kt, v_text=vt, q_text=qt)
+        else:
+            o = lv.lvsa_attention(q, k, v, m)
+        assert torch.isfinite(o.float()).all() and o.float().abs().max().item() <= vmax * 1.01
+        rows = [set(r) for r in om.build_frame_mask(T, P, W, 1, kfi, offset=off).rows]
+        frames = _sweep_frames(T, P, kfi, off)
+        ro, _ = oa.per_frame_sdpa(qf, kf, vf, rows, P, k_extra=kt.float() if n_txt else None,
+                                  v_extra=vt.float() if n_txt else None, frames=frames)
+        _close(o, ro, f"{name} offset {off} frames {frames}")
+        if n_txt and off == offsets[0]:
+            rto, _ = oa.text_row_attention(qt.float(), kf, vf, kt.float(), vt.float())
+            _close(ot, rto, f"{name} text rows")
 
 
 SPLIT = [

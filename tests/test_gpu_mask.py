@@ -177,3 +177,71 @@ def test_plan_block_csr_at_baseline(name, T, P, W, kfi, offs, b, gpu):
             assert plan.tile_indptr.cpu().tolist() == indptr, (name, off, bq, bk)
             got = (plan.entries[: indptr[-1], 0].cpu().numpy().astype(np.int64) & 0x7FFFFFFF).tolist()
             assert got == cols, (name, off, bq, bk)
+
+
+def test_window_golden_arbitrary_global_sets(golden, gpu):
+    """The reference's window bounds for 600 arbitrary global sets: each set
+    goes in as boundary guards (no anchors, no keyframe grid), so the device's
+    expanded-window tie-break is pinned beyond the anchor + grid sets."""
+    by_pattern = {}
+    for rec in golden["windows"]:
+        by_pattern.setdefault((rec["T"], rec["W"], tuple(rec["G"]), rec["expand"]), []).append(rec)
+    assert sum(len(v) for v in by_pattern.values()) == 600
+    for (T, W, G, expand), recs in by_pattern.items():
+        p = hip_ops.mask_params(T, 1, W, 0, None, 0, expand, guards=G)
+        dm = hip_ops.mask_build(p, gpu)
+        ng = int(dm.info[2].item())
+        assert dm.global_frames[:ng].tolist() == sorted(G)
+        bounds = dm.window_bounds.tolist()
+        for rec in recs:
+            assert bounds[rec["f"]] == rec["bounds"], rec
+
+
+def test_auto_kfi_golden(golden, gpu):
+    """lvsa_auto_kfi against the reference's compute_auto_kfi outputs."""
+    recs = golden["auto_kfi"]
+    out = torch.full((len(recs),), -7, dtype=torch.int32, device=gpu)
+    for i, r in enumerate(recs):
+        hip_ops.auto_kfi(r["T"], r["W"], r["n_first"], r["ref"], r["scale"], out=out[i:i + 1])
+    assert out.tolist() == [r["kfi"] for r in recs]
+
+
+def test_auto_kfi_sweep(gpu):
+    """Both branches (strict / fallback), the dense cut-off, W = 0, no
+    anchors, T well past the mask limit and budgets from scales below and
+    above 1, against the oracle."""
+    cases = [(T, W, n, ref, sc) for T in list(range(1, 48)) + [60, 97, 257, 1000, 4096, 9999]
+             for W in (0, 1, 3, 12) for n in (0, 1, 4) for ref, sc in ((21, 1.0), (21, 0.45), (33, 1.3), (5, 3.0))]
+    out = torch.empty(len(cases), dtype=torch.int32, device=gpu)
+    for i, c in enumerate(cases):
+        hip_ops.auto_kfi(*c, out=out[i:i + 1])
+    want = [om.compute_auto_kfi(T, W, n, reference_frames=ref, sparsity_scale=sc) for T, W, n, ref, sc in cases]
+    got = out.tolist()
+    bad = [(c, g, w) for c, g, w in zip(cases, got, want) if g != w]
+    assert not bad, bad[:5]
+    assert len(set(want)) > 30
+
+
+@pytest.mark.parametrize("scale", [0.5, 1.0, 1.7])
+def test_mask_auto_kfi_equals_explicit(golden, scale, gpu):
+    """lvsa_mask_build with the device re-tune (kfi derived in the kernel,
+    offset = step % kfi) writes exactly what an explicit build with the
+    oracle's kfi and offset writes, and reports that kfi in info[7]."""
+    for rec in golden["baseline"][::2] + golden["random"][::20]:
+        a = rec["args"]
+        kfi = om.compute_auto_kfi(a["T"], a["W"], a["n_first"], sparsity_scale=scale)
+        for step in (0, 5, 13):
+            common = (a["T"], a["P"], a["W"], a["n_first"])
+            pa = hip_ops.mask_params(*common, None, 0, a["expand"], a["rank"], a["world"], a["guards"] or (),
+                                     auto_step=step, sparsity_scale=scale)
+            pe = hip_ops.mask_params(*common, kfi, step % kfi, a["expand"], a["rank"], a["world"],
+                                     a["guards"] or ())
+            da, de = hip_ops.mask_build(pa, gpu), hip_ops.mask_build(pe, gpu)
+            tag = (str(a), scale, step)
+            assert int(da.info[7].item()) == kfi, tag
+            nnz = int(de.info[0].item())
+            assert da.info[:7].tolist() == de.info[:7].tolist(), tag
+            assert torch.equal(da.frame_indptr, de.frame_indptr), tag
+            assert torch.equal(da.frame_indices[:nnz], de.frame_indices[:nnz]), tag
+            for f in ("compact_frames", "global_frames", "window_bounds", "rel_full", "rel_window"):
+                assert torch.equal(getattr(da, f), getattr(de, f)), (f, tag)

@@ -191,3 +191,21 @@ def test_processor_csr_matches_oracle(cfg, gpu):
             assert all(0 <= c < proc._fi_compact_n for c in row)
         if cfg["W"] == 0:
             assert proc._fi_compact_n == nG
+
+
+def test_retune_derives_kfi_on_the_device(gpu, monkeypatch):
+    """set_window_size / set_sparsity_scale take kfi from lvsa_auto_kfi, not
+    from the host formula (lvsa/lvsa_processor.py:288-360)."""
+    import longvideosparseattention_amd.processor as proc_mod
+
+    def _host_formula(*a, **k):
+        raise AssertionError("host compute_auto_kfi called")
+
+    p = DistributedLVSAProcessor(40, 16, 2, 2, 4, 0, 1, reference_frames=21)
+    monkeypatch.setattr(proc_mod, "compute_auto_kfi", _host_formula)
+    p.set_sparsity_scale(0.6)
+    assert p.key_frame_interval == om.compute_auto_kfi(40, 2, 2, reference_frames=21, sparsity_scale=0.6)
+    p.set_window_size(0)
+    assert p.key_frame_interval == om.compute_auto_kfi(40, 0, 2, reference_frames=21, sparsity_scale=0.6)
+    ref = om.build_frame_mask(40, 16, 0, 2, p.key_frame_interval, offset=0)
+    assert p._global_indices == ref.global_indices

@@ -88,7 +88,7 @@ def run_loop(entries, nk, n_x, seed=0, dt="bf16", **opts):
         for i, b in enumerate((kb0, vb0, kb1, vb1)):
             S[24 + 2 * i], S[25 + 2 * i] = b & 0xFFFFFFFF, b >> 32
         S[32:36] = [256, 256, 256, 256]
-        S[36], S[37], S[39] = nk, n_x, 1024 * w
+        S[36], S[37], S[38], S[39] = nk, n_x, w, 1024 * w
         waves.append(W)
     sim.run(waves)
     O = np.zeros((R, D))
