@@ -173,3 +173,40 @@ def test_wrapper_rejects_csr_with_wrong_row_count():
     indices = torch.tensor([0, 1], dtype=torch.int32)
     with pytest.raises(ValueError, match="M/R = 3"):
         w.plan(indptr, indices, M=192, N=128, R=64, C=64, num_qo_heads=2, num_kv_heads=2, head_dim=128)
+
+
+def test_shim_binds_the_reference_import_names():
+    """shim.install(): ``import flashinfer`` and the plugin's runner module
+    resolve to the HIP wrapper, prefill and runner (the names the reference
+    gates its FlashInfer backends on, lvsa/lvsa_processor.py:30-34,
+    flashinfer_runner.py:21-26), and the SDPA path's module names to this
+    package.  Runs in a fresh interpreter so sys.modules stays clean here."""
+    import subprocess
+    import sys
+    import textwrap
+    code = textwrap.dedent("""
+        import sys
+        sys.modules.pop("flashinfer", None)
+        from longvideosparseattention_amd import shim, block_sparse, sparse_attention, global_kv
+        got = shim.install()
+        assert sorted(got) == ["flashinfer", "lvsa.sparse_attention", "lvsa_vllm_omni.flashinfer_runner",
+                               "lvsa_vllm_omni.global_kv"], got
+        import flashinfer
+        assert flashinfer.BlockSparseAttentionWrapper is block_sparse.BlockSparseAttentionWrapper
+        assert flashinfer.single_prefill_with_kv_cache is block_sparse.single_prefill_with_kv_cache
+        from lvsa_vllm_omni.flashinfer_runner import (FLASHINFER_AVAILABLE, FlashInferDualStreamRunner,
+                                                      get_shared_runner)
+        assert FLASHINFER_AVAILABLE and FlashInferDualStreamRunner is block_sparse.HipDualStreamRunner
+        assert get_shared_runner() is get_shared_runner()
+        from lvsa.sparse_attention import lvsa_sdpa, LVSAMetadata
+        assert lvsa_sdpa is sparse_attention.lvsa_sdpa
+        from lvsa_vllm_omni.global_kv import build_global_kv
+        assert build_global_kv is global_kv.build_global_kv
+        # a second install leaves bound names alone unless asked
+        assert shim.install() == {}
+        assert sorted(shim.install(["flashinfer"], replace=True)) == ["flashinfer"]
+        print("ok")
+    """)
+    root = str(__import__("pathlib").Path(__file__).resolve().parents[1])
+    res = subprocess.run([sys.executable, "-c", code], cwd=root, capture_output=True, text=True, timeout=300)
+    assert res.returncode == 0 and res.stdout.strip().endswith("ok"), res.stderr[-2000:]
