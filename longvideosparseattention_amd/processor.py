@@ -26,6 +26,7 @@ package, so ``__call__`` needs one (``attention`` does not).
 
 from __future__ import annotations
 
+from collections import OrderedDict
 from typing import Any, Optional, Tuple
 
 import torch
@@ -52,6 +53,11 @@ class DistributedLVSAProcessor:
 
     _attention_backend = None
     _parallel_config = None
+    # Parameter sets (window, kfi, sparsity) whose patterns stay cached: the
+    # current one and the one before it (denoising schedules alternate a
+    # windowed and a globals-only band); older sets and their device masks
+    # and plans are dropped, as the reference drops its state on a rebuild.
+    _PATTERN_SETS = 2
 
     def __init__(
         self,
@@ -80,7 +86,7 @@ class DistributedLVSAProcessor:
         self._use_flashinfer = False
         self._geometry_warned = False
         self._dense_plans = {}
-        self._pattern_cache = {}
+        self._pattern_cache: "OrderedDict[tuple, dict]" = OrderedDict()
         # Boundary guards stay fixed across rotations (lvsa_processor.py:135-140).
         self._boundary_guards = compute_boundary_guard_frames(
             total_num_latent_frames, total_num_latent_frames * num_patches // world,
@@ -99,11 +105,17 @@ class DistributedLVSAProcessor:
         Patterns are kept per parameter set: a denoising run cycles through
         ``kfi`` offsets, so every rotation after the first cycle reuses the
         metadata together with its device mask and block plans."""
-        key = (offset, self.window_size, self.key_frame_interval, self._sparsity_scale)
-        meta = self._pattern_cache.get(key)
+        params = (self.window_size, self.key_frame_interval, self._sparsity_scale)
+        per_offset = self._pattern_cache.get(params)
+        if per_offset is None:
+            per_offset = self._pattern_cache[params] = {}
+            while len(self._pattern_cache) > self._PATTERN_SETS:
+                self._pattern_cache.popitem(last=False)
+        else:
+            self._pattern_cache.move_to_end(params)
+        meta = per_offset.get(offset)
         if meta is None:
-            meta = self._build_uncached(offset)
-            self._pattern_cache[key] = meta
+            meta = per_offset[offset] = self._build_uncached(offset)
         return meta
 
     def _build_uncached(self, offset: int) -> LVSAMetadata:

@@ -179,6 +179,24 @@ class TestDynamicReconfiguration:
         p.set_sparsity_scale(0.5)
         assert p._metadata is m
 
+    def test_pattern_cache_keeps_two_parameter_sets(self):
+        """Patterns of at most the current and the previous (window, kfi,
+        sparsity) set stay cached; switching back to the previous set reuses
+        its metadata, older sets are dropped."""
+        p = _proc(T=81, W=3, n_first=1, kfi=None)
+        for scale in (0.5, 0.7, 0.9, 1.3, 0.5):
+            p.set_sparsity_scale(scale)
+            assert len(p._pattern_cache) <= 2
+        m = p._metadata
+        p.set_window_size(0)
+        p.set_window_size(3)
+        assert p._metadata is m
+        p.set_sparsity_scale(2.0)
+        p.set_sparsity_scale(0.25)
+        p.set_sparsity_scale(0.5)
+        assert p._metadata is not m
+        _assert_matches_oracle(p)
+
     def test_window_change_shrinks_compact_set(self):
         p = _proc(W=3)
         before = p._fi_compact_n
