@@ -11,9 +11,12 @@ is reported separately.  Inputs are resident in HBM when timing starts.
 
 Prints ONE JSON line: metric/value (effective TFLOP/s on active 128-blocks,
 BASELINE's metric), ms per call, the roofline of the attention kernel
-(algorithmic FLOPs per launch / HIP-event launch time vs the 2.5 PFLOP/s
-dense bf16 MFMA peak of MI355X) and a CPU baseline (the repository's fp32
-CPU restatement timed on the host cores over a bounded sample).
+(algorithmic FLOPs per launch / HIP-event time per call on the launch stream,
+vs the 2.5 PFLOP/s dense bf16 MFMA peak of MI355X; HBM traffic from a
+committed rocprof counters file of the same build) and a CPU baseline (the
+repository's fp32 CPU restatement timed on the host cores over a bounded
+sample, extrapolated to ms per call, plus masked SDPA at the reference's CPU
+configuration).
 """
 
 from __future__ import annotations
@@ -81,38 +84,69 @@ def copy_calibration(mib: int) -> int:
     return 0
 
 
+def source_hash() -> str:
+    """Hash of the HIP sources and the build script: names the build a
+    committed counters file was measured on."""
+    import hashlib
+
+    h = hashlib.sha256()
+    pkg = os.path.join(ROOT, "longvideosparseattention_amd")
+    csrc = os.path.join(pkg, "csrc")
+    files = sorted(f for f in os.listdir(csrc) if f.endswith((".hip", ".h", ".inc", ".py")))
+    for name in files + ["../build_lib.py", "../../include/lvsa_amd.h"]:
+        with open(os.path.join(csrc, name), "rb") as f:
+            h.update(name.encode() + b"\0" + f.read())
+    return h.hexdigest()[:16]
+
+
 def profiled_traffic(config: str):
-    """HBM bytes per attention launch for `config`, as measured by the two
-    rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE, each scaled by the same
-    counter on a 1 GiB copy) summarised under profiles/; None if absent."""
+    """HBM bytes per attention launch for `config` from the two rocprofv3
+    --pmc runs summarised under profiles/ (FETCH_SIZE, WRITE_SIZE, each scaled
+    by the same counter on a 1 GiB copy), used only when that file was
+    measured on this build (its source_hash equals source_hash()).
+    Returns (bytes or None, file, note)."""
     import glob
     import re
 
+    here = source_hash()
     for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "*_counters.md"))):
         with open(path) as f:
-            m = re.search(r"traffic_bytes_per_launch\[" + re.escape(config) + r"\]\s*=\s*(\d+)", f.read())
-        if m:
-            return int(m.group(1)), os.path.relpath(path, ROOT)
-    return None, None
+            text = f.read()
+        m = re.search(r"traffic_bytes_per_launch\[" + re.escape(config) + r"\]\s*=\s*(\d+)", text)
+        if not m:
+            continue
+        rel = os.path.relpath(path, ROOT)
+        hm = re.search(r"source_hash\s*=\s*([0-9a-f]+)", text)
+        if hm is None or hm.group(1) != here:
+            return None, rel, f"measured on another build ({hm.group(1) if hm else 'unrecorded'} != {here})"
+        return int(m.group(1)), rel, "same build"
+    return None, None, "no counters file for this configuration"
 
 
-def cpu_baseline(q, k, v, qt, kt, vt, meta, budget_s: float):
-    """Time the fp32 CPU restatement (per-frame gather + dense attention) of the
-    same call on the host cores over a bounded sample of (head, query frame)
-    pairs; return its throughput in effective TFLOP/s (token-exact work)."""
+def cpu_baseline(q, k, v, qt, kt, vt, meta, budget_s: float, f_block_per_call: float):
+    """The fp32 CPU restatement of the call (per-frame gather + dense
+    attention, the reference's lvsa_sdpa loop) on the host cores.
+
+    A bounded sample of (head, query frame) pairs is timed and extrapolated
+    linearly to the whole call by H*T / pairs; text-query rows (dense over all
+    keys) are timed for one head and scaled by H.  Reported as ms per call and
+    as effective TFLOP/s with the GPU line's FLOP count.  Also times fp32
+    masked SDPA with the full [2304, 2304] token mask at the reference's CPU
+    configuration (1 warm-up, median of 5)."""
+    import torch.nn.functional as F
+
     from oracle import attention as oa  # CPU-baseline leg only
+    from oracle import lvsa_mask as om
 
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
     P = meta.num_patches
     T = meta.total_latent_frames
+    H = q.shape[2]
     rows = [set(meta._attended_rows[f]) for f in range(T)]
-    D = q.shape[3]
-    work = 0
     n_pairs = 0
     t0 = time.perf_counter()
-    h = 0
-    while time.perf_counter() - t0 < budget_s and h < q.shape[2]:
+    for h in range(H):
         for f in range(T):
             qs = slice(f * P, (f + 1) * P)
             parts_k = [k[:, g * P:(g + 1) * P, h:h + 1] for g in sorted(rows[f])]
@@ -120,17 +154,41 @@ def cpu_baseline(q, k, v, qt, kt, vt, meta, budget_s: float):
             if kt is not None:
                 parts_k.append(kt[:, :, h:h + 1])
                 parts_v.append(vt[:, :, h:h + 1])
-            kc, vc = torch.cat(parts_k, 1), torch.cat(parts_v, 1)
-            oa.dense_attention(q[:, qs, h:h + 1], kc, vc)
-            work += 4 * D * P * kc.shape[1]
+            oa.dense_attention(q[:, qs, h:h + 1], torch.cat(parts_k, 1), torch.cat(parts_v, 1))
             n_pairs += 1
-            if time.perf_counter() - t0 >= budget_s:
+            if time.perf_counter() - t0 >= 0.8 * budget_s:
                 break
-        h += 1
-    dt = time.perf_counter() - t0
-    return {"value": work / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": f"{n_pairs} (head, query-frame) pairs of the same call in fp32 "
-                      f"({work / 1e9:.1f} GFLOP token-exact, {dt:.1f} s), text rows excluded"}
+        if time.perf_counter() - t0 >= 0.8 * budget_s:
+            break
+    pair_ms = 1e3 * (time.perf_counter() - t0) / n_pairs
+    text_ms = 0.0
+    if qt is not None:
+        t1 = time.perf_counter()
+        oa.text_row_attention(qt[:, :, :1], k[:, :, :1], v[:, :, :1], kt[:, :, :1], vt[:, :, :1])
+        text_ms = 1e3 * (time.perf_counter() - t1) * H
+    factor = H * T / n_pairs
+    ms_call = pair_ms * H * T + text_ms
+
+    # reference CPU configuration: 12 heads, D 128, 9 frames x 256, kfi 4 at step 3, window 1
+    g = torch.Generator().manual_seed(0)
+    cq, ck, cv = (torch.randn(1, 12, 2304, 128, generator=g) for _ in range(3))
+    rel = om.build_frame_mask(9, 256, 1, 1, 4, offset=3).rows
+    mask = torch.from_numpy(om.token_mask([set(r) for r in rel], 256, 2304, 2304))
+    times = []
+    for i in range(6):
+        t1 = time.perf_counter()
+        F.scaled_dot_product_attention(cq, ck, cv, attn_mask=mask)
+        if i:
+            times.append(1e3 * (time.perf_counter() - t1))
+    sdpa_ms = sorted(times)[len(times) // 2]
+    return {"value": round(f_block_per_call / (ms_call * 1e-3) / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
+            "kind": "port", "ms_per_call": round(ms_call, 1), "extrapolation_factor": round(factor, 2),
+            "sample": f"{n_pairs} of {H * T} (head, query-frame) pairs of the same call, fp32 per-frame "
+                      f"gather + dense attention, {pair_ms:.2f} ms each, x{factor:.2f} to the call"
+                      + (f"; text rows timed for 1 head, x{H}" if qt is not None else ""),
+            "cpu_config_masked_sdpa_ms": round(sdpa_ms, 2),
+            "cpu_config_masked_sdpa": "fp32 F.scaled_dot_product_attention, 12 heads, [2304, 2304] token mask "
+                                      "(9 frames x 256, kfi 4 at step 3, window 1), median of 5 after 1 warm-up"}
 
 
 def main(argv=None) -> int:
@@ -186,6 +244,7 @@ def main(argv=None) -> int:
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
+    # events on the stream the kernels are launched on (torch's current stream)
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     ev0.record()
@@ -201,8 +260,12 @@ def main(argv=None) -> int:
     value = fb / wall / 1e12
     achieved = fb / (ev_ms * 1e-3 * args.steps) / 1e12
     bytes_per_call = 4 * (N + n_text) * H * D * 2
-    traffic, traffic_src = profiled_traffic(args.config)
-    kernel = "attn_fwd_pp_kernel" if lvops.attn_block_q(D) == 256 else "attn_fwd_kernel"
+    traffic, traffic_src, traffic_note = profiled_traffic(args.config if args.window is None else
+                                                          f"{args.config}_w{W}")
+    kernel = {128: "attn_fwd_stream_kernel", 64: "attn_fwd_pp_kernel", 96: "attn_fwd_pp_kernel"}.get(
+        D, "attn_fwd_kernel")
+    if D == 128 and os.environ.get("LVSA_ATTN_KERNEL") == "pp":
+        kernel = "attn_fwd_pp_kernel"
 
     line = {
         "metric": "block-sparse attn ms/call + effective TFLOP/s (% bf16 MFMA peak), "
@@ -229,16 +292,20 @@ def main(argv=None) -> int:
         # build also pays the one-time library load and code-object upload
         "mask_and_plan_build_ms": round(sorted(build_ms[1:] or build_ms)[len(build_ms[1:] or build_ms) // 2], 3),
         "mask_and_plan_first_build_ms": round(build_ms[0], 3),
+        # achieved = block FLOPs / the HIP-event span of the timed calls on the
+        # launch stream (the attention kernel, plus the text merge kernel
+        # where text tiles are split); rocprof kernel averages: profiles/
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": traffic,
-                     "traffic_source": traffic_src, "kernel": kernel, "kernel_ms": round(ev_ms, 4)},
+                     "traffic_source": traffic_src, "traffic_note": traffic_note, "kernel": kernel,
+                     "event_ms_per_call": round(ev_ms, 4), "build": source_hash()},
     }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(q.float().cpu(), k.float().cpu(), v.float().cpu(),
                                             None if qt is None else qt.float().cpu(),
                                             None if kt is None else kt.float().cpu(),
                                             None if vt is None else vt.float().cpu(),
-                                            metas[offsets[0]], args.cpu_seconds)
+                                            metas[offsets[0]], args.cpu_seconds, fb / args.steps)
     else:
         line["cpu_baseline"] = None
     print(json.dumps(line), flush=True)
