@@ -109,7 +109,7 @@ def profiled_traffic(config: str):
     import re
 
     here = source_hash()
-    for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "*_counters.md"))):
+    for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "*.md"))):
         with open(path) as f:
             text = f.read()
         m = re.search(r"traffic_bytes_per_launch\[" + re.escape(config) + r"\]\s*=\s*(\d+)", text)
