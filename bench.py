@@ -262,9 +262,9 @@ def main(argv=None) -> int:
     bytes_per_call = 4 * (N + n_text) * H * D * 2
     traffic, traffic_src, traffic_note = profiled_traffic(args.config if args.window is None else
                                                           f"{args.config}_w{W}")
-    kernel = {128: "attn_fwd_stream_kernel", 64: "attn_fwd_pp_kernel", 96: "attn_fwd_pp_kernel"}.get(
+    kernel = {128: "attn_fwd_stream_kernel", 64: "attn_fwd_stream_kernel", 96: "attn_fwd_pp_kernel"}.get(
         D, "attn_fwd_kernel")
-    if D == 128 and os.environ.get("LVSA_ATTN_KERNEL") == "pp":
+    if D in (64, 128) and os.environ.get("LVSA_ATTN_KERNEL") == "pp":
         kernel = "attn_fwd_pp_kernel"
 
     line = {

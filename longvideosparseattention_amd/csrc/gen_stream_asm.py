@@ -1,21 +1,23 @@
-"""Generate the key loop of the single-stream D = 128 attention kernel.
+"""Generate the key loop of the single-stream attention kernel (D = 64 and 128).
 
     python gen_stream_asm.py [out.inc]   (default: lvsa_attn_stream_body.inc beside this file)
 
 The loop is hand-scheduled gfx950 assembly, emitted as the body of one inline
 asm statement of ``attn_fwd_stream_kernel`` (lvsa_attn_stream.h), whose
-operands pin every register this text names.  Each of the 8 waves of a
-work-group owns 32 query rows of a 256-row tile and walks the tile's 64-key
-blocks as two 32-key sub-blocks; sub-iteration i issues, as one stream,
+operands pin every register this text names; the operand lists are emitted
+here too (``LVSA_STREAM<D>_OUTPUTS`` / ``_INPUTS`` / ``_CLOBBERS``), so the
+register map lives in one place.  Each of the 8 waves of a work-group owns
+32 query rows of a 256-row tile and walks the tile's 64-key blocks as two
+32-key sub-blocks; sub-iteration i issues, as one stream,
 
-    QK(i)   S = K Q^T of sub-block i          8 MFMAs   (K from LDS)
-    SM(i-1) softmax of sub-block i - 1        ~50 VALU  (P = 2^(S*cs - m))
-    PV(i-2) O += V^T P^T of sub-block i - 2   8 MFMAs   (V^T from LDS)
+    QK(i)   S = K Q^T of sub-block i          D/16 MFMAs  (K from LDS)
+    SM(i-1) softmax of sub-block i - 1        ~50 VALU    (P = 2^(S*cs - m))
+    PV(i-2) O += V^T P^T of sub-block i - 2   D/16 MFMAs  (V^T from LDS)
 
 so every wave keeps the matrix core and the VALU busy at once, and the two
 waves that share a SIMD fill each other's gaps.  Per 64-key block: one
-work-group barrier, four 1 KiB global->LDS copies per wave (block j + 2 into
-a 4-stage ring) and one scalar load of a plan entry.
+work-group barrier, D/64 1 KiB global->LDS copies of K and as many of V per
+wave (block j + 2 into a 4-stage ring) and one scalar load of a plan entry.
 
 Softmax without a row max: P is formed against the running max m of the
 earlier blocks; m has to move only if some P exceeds 2^8, and then the
@@ -34,16 +36,16 @@ states later; a v_exp result 1 state later; VALU results feed MFMAs a
 sub-iteration later; M0 writes are followed by one state before an LDS copy;
 v_permlane32_swap is fenced by two states on each side.
 
-Register map (VGPRs; the kernel's operands pin them):
-  v[0:63] O (4 d-tiles x 16)      v[64:95] Q (8 k-steps x 4)
-  v[96:111] S_A, v[112:127] S_B   v[128:135] P_A, v[136:143] P_B
-  v[144:175] LDS operand slots    v[176:183] K read offsets, v[184:191] V^T
-  v192 m, v193 l, v194-195 partial row sums, v196 copy row, v197 copy chunk
-  v198-199 copy offsets (K, V), v200 tile row, v201 4*h, v202 -inf, v203
-  mask temp, v[204:207] RARE temps, v[208:223] softmax temps
+Register map (VGPRs; the kernel's operands pin them), D = 128 (D = 64):
+  O (D/32 d-tiles x 16) v[0:63] (v[0:31]); Q (D/16 k-steps x 4) v[64:95]
+  (v[32:47]); then two S tiles (16 each), two P tiles (8 each), eight LDS
+  operand slots (4 each), the K read offsets (one per k-step), the V^T read
+  offsets (two per d-tile), then m, l, two partial row sums, the copy row and
+  chunk, the two copy offsets, the tile row, 4*h, -inf, a mask temp, four
+  RARE temps and sixteen softmax temps: 224 (168) VGPRs in all.
 SGPRs: s[20:21] entry pointer, s22 blocks, s23 scale*log2(e), s[24:31] K/V
-bases (video, extra), s32-35 row strides, s36-37 source lengths, s39 LDS
-copy base of the wave; s40-s95 scratch.
+bases (video, extra), s32-35 row strides, s36-37 source lengths, s38 wave,
+s39 LDS copy base of the wave; s40-s95 scratch.
 """
 
 from __future__ import annotations
@@ -51,22 +53,53 @@ from __future__ import annotations
 import sys
 from pathlib import Path
 
-# ── register map ──
-O, Q, SA, SB, PA, PB, OPS, NSLOT = 0, 64, 96, 112, 128, 136, 144, 8
-KOFF, VOFFA, VOFFB = 176, 184, 188
-VM, VL, LS0, LS1, DMAROW, C16, DK, DV = 192, 193, 194, 195, 196, 197, 198, 199
-ROW, H4, NEGINF, VT, RT, T = 200, 201, 202, 203, 204, 208
+# ── SGPR map ──
 S_EPTR, S_N, S_CS = 20, 22, 23
 S_KB0, S_VB0, S_KB1, S_VB1 = 24, 26, 28, 30
 S_KRS0, S_VRS0, S_KRS1, S_VRS1, S_NK, S_NX, S_WAVE, S_LDSK = 32, 33, 34, 35, 36, 37, 38, 39
 S_J, S_NM1, S_CUR, S_ENT, S_RK, S_RV = 40, 41, 42, 44, 52, 56
 S_SOK, S_SOV, S_KRSC = 60, 62, 64  # copy soffsets (K: 60, 61; V: 62, 63); strides, 32-row strides
 S_RET = 76
-TILE, VBASE = 16384, 65536        # bytes of a K (V) block of 64 rows x 256 B; V tiles start at 64 KiB
-LA = 6                            # MFMAs of LDS operand lookahead (< NSLOT)
-
-CLOBBER_V = list(range(96, 176)) + [LS0, LS1, DK, DV] + list(range(204, 224))
 CLOBBER_S = list(range(40, 96))
+NSLOT = 8                         # LDS operand slots
+LA = 3                            # MFMAs of LDS operand lookahead (< NSLOT); 3 measured best:
+                                  # 2.5% (D = 128) and 4.3% (D = 64) fewer cycles than 6
+
+
+class Layout:
+    """Head-size dependent shapes and the VGPR map."""
+
+    def __init__(self, D: int):
+        assert D in (64, 128)
+        self.D = D
+        self.NQK = D // 16                # MFMA k-steps of a score tile
+        self.NDT = D // 32                # 32-wide d-tiles of O
+        self.RB = 2 * D                   # bytes per K/V row in LDS
+        self.TILE = 64 * self.RB          # one K or V block
+        self.VBASE = 4 * self.TILE        # V stages follow the 4 K stages
+        self.NCP = D // 64                # 1 KiB copies of K (and of V) per wave and block
+        r = 0
+
+        def take(n: int) -> int:
+            nonlocal r
+            r += n
+            return r - n
+        self.O = take(16 * self.NDT)
+        self.Q = take(4 * self.NQK)
+        self.SA, self.SB = take(16), take(16)
+        self.PA, self.PB = take(8), take(8)
+        self.OPS = take(4 * NSLOT)
+        self.KOFF = take(self.NQK)
+        self.VOFFA = take(self.NDT)
+        self.VOFFB = take(self.NDT)
+        self.VM, self.VL, self.LS0, self.LS1 = take(1), take(1), take(1), take(1)
+        self.DMAROW, self.C16, self.DK, self.DV = take(1), take(1), take(1), take(1)
+        self.ROW, self.H4, self.NEGINF, self.VT = take(1), take(1), take(1), take(1)
+        self.RT = take(4)
+        self.T = take(16)
+        self.NVGPR = r
+        self.CLOBBER_V = (list(range(self.SA, self.KOFF)) + [self.LS0, self.LS1, self.DK, self.DV] +
+                          list(range(self.RT, self.NVGPR)))
 
 
 def vr(a: int, n: int = 1) -> str:
@@ -82,11 +115,12 @@ def lbl(name: str) -> str:
 
 
 class Gen:
-    def __init__(self, dt: str, pad: bool = False, always_rare: bool = False, la: int = LA,
+    def __init__(self, dt: str, D: int = 128, pad: bool = False, always_rare: bool = False, la: int = LA,
                  pv_b128: bool = False, no_softmax: bool = False, order: str = "group",
                  no_barrier: bool = False, no_decode: bool = False, no_exp: bool = False):
         assert dt in ("bf16", "f16")
         self.dt = dt
+        self.L = Layout(D)
         self.pad = pad                  # diagnostics: 16 wait states after every MFMA
         self.always_rare = always_rare  # diagnostics: exact row max on every sub-block
         self.la = la                    # MFMAs of LDS operand lookahead
@@ -109,16 +143,17 @@ class Gen:
     # ── softmax ──
     def softmax_ops(self, S: int, P: int) -> list[str]:
         """P = 2^(S*cs - m) as bf16/f16 pairs; this sub-block's row sum in LS0 + LS1."""
+        L = self.L
         if self.no_softmax:
-            return [f"v_mov_b32 {vr(LS0)}, 0", f"v_mov_b32 {vr(LS1)}, 0"]
+            return [f"v_mov_b32 {vr(L.LS0)}, 0", f"v_mov_b32 {vr(L.LS1)}, 0"]
         cvt = "v_cvt_pk_bf16_f32" if self.dt == "bf16" else "v_cvt_pk_f16_f32"
         one = "0x3f803f80" if self.dt == "bf16" else "0x3c003c00"
         dot = "v_dot2c_f32_bf16" if self.dt == "bf16" else "v_dot2c_f32_f16"
-        fma = lambda k: f"v_fma_f32 {vr(T + k)}, {vr(S + k)}, {sr(S_CS)}, -{vr(VM)}"  # noqa: E731
-        exp = lambda k: ("s_nop 0" if self.no_exp else f"v_exp_f32 {vr(T + k)}, {vr(T + k)}")  # noqa: E731
-        pk = lambda q: f"{cvt} {vr(P + q)}, {vr(T + 2 * q)}, {vr(T + 2 * q + 1)}"  # noqa: E731
-        d2 = lambda q: f"{dot} {vr(LS0 + (q & 1))}, {one}, {vr(P + q)}"  # noqa: E731
-        ops = [f"v_mov_b32 {vr(LS0)}, 0", f"v_mov_b32 {vr(LS1)}, 0"]
+        fma = lambda k: f"v_fma_f32 {vr(L.T + k)}, {vr(S + k)}, {sr(S_CS)}, -{vr(L.VM)}"  # noqa: E731
+        exp = lambda k: ("s_nop 0" if self.no_exp else f"v_exp_f32 {vr(L.T + k)}, {vr(L.T + k)}")  # noqa: E731
+        pk = lambda q: f"{cvt} {vr(P + q)}, {vr(L.T + 2 * q)}, {vr(L.T + 2 * q + 1)}"  # noqa: E731
+        d2 = lambda q: f"{dot} {vr(L.LS0 + (q & 1))}, {one}, {vr(P + q)}"  # noqa: E731
+        ops = [f"v_mov_b32 {vr(L.LS0)}, 0", f"v_mov_b32 {vr(L.LS1)}, 0"]
         if self.order == "mix":
             # one exponential between two other ops: fma k+2, exp k; packs and dots
             # trail their exponentials by two
@@ -146,14 +181,15 @@ class Gen:
         """Rare-case test on this sub-block's row sum, then l += sum.  Runs after
         the last PV MFMA of the sub-iteration, so RARE rescales every
         contribution made with the old m."""
+        L = self.L
         self.stubs += [f"{lbl('RSTUB_' + site)}:", f"s_call_b64 {sr(S_RET, 2)}, {lbl('RARE_' + sset)}",
                        f"s_branch {lbl('RRET_' + site)}"]
         return ["s_nop 2",                                         # dot2 result -> VALU: 3 states
-                f"v_add_f32 {vr(LS0)}, {vr(LS0)}, {vr(LS1)}",
-                f"v_cmp_nge_f32 vcc, 0x43800000, {vr(LS0)}",      # !(256 >= ls): ls > 256 or NaN
+                f"v_add_f32 {vr(L.LS0)}, {vr(L.LS0)}, {vr(L.LS1)}",
+                f"v_cmp_nge_f32 vcc, 0x43800000, {vr(L.LS0)}",    # !(256 >= ls): ls > 256 or NaN
                 f"s_branch {lbl('RSTUB_' + site)}" if self.always_rare else f"s_cbranch_vccnz {lbl('RSTUB_' + site)}",
                 f"{lbl('RRET_' + site)}:",
-                f"v_add_f32 {vr(VL)}, {vr(VL)}, {vr(LS0)}"]
+                f"v_add_f32 {vr(L.VL)}, {vr(L.VL)}, {vr(L.LS0)}"]
 
     def mask_check(self, site: str, sset: str, desc: int, half: int) -> list[str]:
         self.stubs += [f"{lbl('MSTUB_' + site)}:", f"s_mov_b32 s91, {sr(desc)}", f"s_mov_b32 s75, {32 * half}",
@@ -163,6 +199,8 @@ class Gen:
 
     def rare_routine(self, S: int, P: int, name: str) -> list[str]:
         """True row max of the sub-block, m -> max(m, max*cs), O and l rescaled, P recomputed."""
+        L = self.L
+        RT = L.RT
         r = [f"{lbl(name)}:", "s_nop 15", "s_nop 7",
              f"v_max3_f32 {vr(RT)}, {vr(S)}, {vr(S + 1)}, {vr(S + 2)}",
              f"v_max3_f32 {vr(RT + 1)}, {vr(S + 3)}, {vr(S + 4)}, {vr(S + 5)}",
@@ -178,15 +216,15 @@ class Gen:
              "s_nop 1",
              f"v_max_f32 {vr(RT)}, {vr(RT)}, {vr(RT + 1)}",       # row max over both lane halves
              f"v_mul_f32 {vr(RT)}, {sr(S_CS)}, {vr(RT)}",
-             f"v_max_f32 {vr(RT)}, {vr(VM)}, {vr(RT)}",           # m_new
-             f"v_sub_f32 {vr(RT + 1)}, {vr(VM)}, {vr(RT)}",
+             f"v_max_f32 {vr(RT)}, {vr(L.VM)}, {vr(RT)}",         # m_new
+             f"v_sub_f32 {vr(RT + 1)}, {vr(L.VM)}, {vr(RT)}",
              f"v_exp_f32 {vr(RT + 1)}, {vr(RT + 1)}",             # alpha = 2^(m - m_new)
-             f"v_mov_b32 {vr(VM)}, {vr(RT)}",
+             f"v_mov_b32 {vr(L.VM)}, {vr(RT)}",
              "s_nop 0",
-             f"v_mul_f32 {vr(VL)}, {vr(RT + 1)}, {vr(VL)}"]
-        r += [f"v_mul_f32 {vr(O + k)}, {vr(RT + 1)}, {vr(O + k)}" for k in range(64)]
+             f"v_mul_f32 {vr(L.VL)}, {vr(RT + 1)}, {vr(L.VL)}"]
+        r += [f"v_mul_f32 {vr(L.O + k)}, {vr(RT + 1)}, {vr(L.O + k)}" for k in range(16 * L.NDT)]
         r += self.softmax_ops(S, P)
-        r += ["s_nop 2", f"v_add_f32 {vr(LS0)}, {vr(LS0)}, {vr(LS1)}", f"s_setpc_b64 {sr(S_RET, 2)}"]
+        r += ["s_nop 2", f"v_add_f32 {vr(L.LS0)}, {vr(L.LS0)}, {vr(L.LS1)}", f"s_setpc_b64 {sr(S_RET, 2)}"]
         return r
 
     def mask_routine(self, S: int, name: str) -> list[str]:
@@ -195,27 +233,28 @@ class Gen:
         Row part b = tile rows >= qs; keys below kb take the part's lo bit, the rest
         its hi bit (bits a.lo, a.hi, b.lo, b.hi).  Element k of the sub-block holds key
         32*half + 8*(k/4) + 4*h + k%4."""
+        L = self.L
         r = [f"{lbl(name)}:",
              "s_bfe_u32 s88, s91, 0x80008",       # kb
              "s_bfe_u32 s89, s91, 0x80010",       # qs
              "s_bfe_u32 s90, s91, 0x40002",       # allow bits
              "s_sub_u32 s88, s88, s75",
-             f"v_cmp_ge_u32_e64 s[78:79], {vr(ROW)}, s89",   # lanes of part b
+             f"v_cmp_ge_u32_e64 s[78:79], {vr(L.ROW)}, s89",   # lanes of part b
              "s_bitcmp1_b32 s90, 0", "s_cselect_b64 s[92:93], -1, 0", "s_andn2_b64 s[92:93], s[92:93], s[78:79]",
              "s_bitcmp1_b32 s90, 2", "s_cselect_b64 s[94:95], -1, 0", "s_and_b64 s[94:95], s[94:95], s[78:79]",
              "s_or_b64 s[80:81], s[92:93], s[94:95]",      # lanes whose lo keys are allowed
              "s_bitcmp1_b32 s90, 1", "s_cselect_b64 s[92:93], -1, 0", "s_andn2_b64 s[92:93], s[92:93], s[78:79]",
              "s_bitcmp1_b32 s90, 3", "s_cselect_b64 s[94:95], -1, 0", "s_and_b64 s[94:95], s[94:95], s[78:79]",
              "s_or_b64 s[82:83], s[92:93], s[94:95]",      # lanes whose hi keys are allowed
-             f"v_sub_u32 {vr(VT)}, s88, {vr(H4)}"]          # kb - 32*half - 4h
+             f"v_sub_u32 {vr(L.VT)}, s88, {vr(L.H4)}"]      # kb - 32*half - 4h
         for k in range(16):
             ck = 8 * (k // 4) + (k % 4)
-            r += [f"v_cmp_lt_i32 vcc, {ck}, {vr(VT)}",      # key below kb
+            r += [f"v_cmp_lt_i32 vcc, {ck}, {vr(L.VT)}",    # key below kb
                   "s_and_b64 s[84:85], vcc, s[80:81]",
                   "s_andn2_b64 s[86:87], s[82:83], vcc",
                   "s_or_b64 s[84:85], s[84:85], s[86:87]",
                   "s_nop 0",
-                  f"v_cndmask_b32_e64 {vr(S + k)}, {vr(NEGINF)}, {vr(S + k)}, s[84:85]"]
+                  f"v_cndmask_b32_e64 {vr(S + k)}, {vr(L.NEGINF)}, {vr(S + k)}, s[84:85]"]
         r += [f"s_setpc_b64 {sr(S_RET, 2)}"]
         return r
 
@@ -226,7 +265,7 @@ class Gen:
         moves the soffsets; a change of source (video <-> extra rows) calls SWITCH."""
         self.stubs += [f"{lbl('SWSTUB_' + site)}:", f"s_call_b64 {sr(S_RET, 2)}, {lbl('SWITCH')}",
                        f"s_branch {lbl('SWRET_' + site)}"]
-        return [
+        r = [
             f"s_lshr_b32 s74, {sr(x)}, 31",
             f"s_cmp_lg_u32 s74, {sr(S_CUR)}",
             f"s_cbranch_scc1 {lbl('SWSTUB_' + site)}",
@@ -234,13 +273,17 @@ class Gen:
             f"s_and_b32 s73, {sr(x)}, 0x7fffffff",
             "s_lshl_b32 s73, s73, 6",                                  # first row of the block
             f"s_mul_i32 {sr(S_SOK)}, s73, {sr(S_KRSC)}",
-            f"s_add_u32 {sr(S_SOK + 1)}, {sr(S_SOK)}, {sr(S_KRSC + 2)}",  # + 32 rows
-            f"s_mul_i32 {sr(S_SOV)}, s73, {sr(S_KRSC + 1)}",
-            f"s_add_u32 {sr(S_SOV + 1)}, {sr(S_SOV)}, {sr(S_KRSC + 3)}",
         ]
+        if self.L.NCP == 2:
+            r.append(f"s_add_u32 {sr(S_SOK + 1)}, {sr(S_SOK)}, {sr(S_KRSC + 2)}")  # + 32 rows
+        r.append(f"s_mul_i32 {sr(S_SOV)}, s73, {sr(S_KRSC + 1)}")
+        if self.L.NCP == 2:
+            r.append(f"s_add_u32 {sr(S_SOV + 1)}, {sr(S_SOV)}, {sr(S_KRSC + 3)}")
+        return r
 
     def switch_routine(self) -> list[str]:
         """Buffer resources, row strides and lane copy offsets of key source s74."""
+        L = self.L
         return [
             f"{lbl('SWITCH')}:",
             f"s_mov_b32 {sr(S_CUR)}, s74",
@@ -258,44 +301,46 @@ class Gen:
             f"s_mov_b32 {sr(S_RV + 3)}, 0x20000",
             f"s_lshl_b32 {sr(S_KRSC + 2)}, {sr(S_KRSC)}, 5",
             f"s_lshl_b32 {sr(S_KRSC + 3)}, {sr(S_KRSC + 1)}, 5",
-            f"v_mad_u32_u24 {vr(DK)}, {vr(DMAROW)}, {sr(S_KRSC)}, {vr(C16)}",
-            f"v_mad_u32_u24 {vr(DV)}, {vr(DMAROW)}, {sr(S_KRSC + 1)}, {vr(C16)}",
+            f"v_mad_u32_u24 {vr(L.DK)}, {vr(L.DMAROW)}, {sr(S_KRSC)}, {vr(L.C16)}",
+            f"v_mad_u32_u24 {vr(L.DV)}, {vr(L.DMAROW)}, {sr(S_KRSC + 1)}, {vr(L.C16)}",
             "s_nop 1",
             f"s_setpc_b64 {sr(S_RET, 2)}",
         ]
 
-    @staticmethod
-    def copy(stage: int, k: int) -> list[str]:
-        """Copy instruction k of a block into `stage`: k = 0, 1 K rows 32k + 4*wave + lane/16,
-        k = 2, 3 the same V rows."""
-        v, ii = k >> 1, k & 1
-        lds = (VBASE if v else 0) + stage * TILE + ii * 8192
+    def copy(self, stage: int, k: int) -> list[str]:
+        """Copy instruction k of a block into `stage`: the first NCP copy K, the
+        rest V; copy ii of a tensor fills LDS KiB 8*ii + wave of the block, i.e.
+        rows 32*ii + 4*wave + lane/16 (D = 128) or 8*wave + lane/8 (D = 64)."""
+        L = self.L
+        v, ii = k // L.NCP, k % L.NCP
+        lds = (L.VBASE if v else 0) + stage * L.TILE + ii * 8192
         rs = S_RV if v else S_RK
         so = sr((S_SOV if v else S_SOK) + ii)
         return [f"s_add_u32 m0, {sr(S_LDSK)}, {lds}", "s_nop 0",
-                f"buffer_load_dwordx4 {vr(DV if v else DK)}, {sr(rs, 4)}, {so} offen lds"]
+                f"buffer_load_dwordx4 {vr(L.DV if v else L.DK)}, {sr(rs, 4)}, {so} offen lds"]
 
     # ── an MFMA stream with its operand reads and the interleaved work ──
     def stream(self, mfmas: list[tuple], fill: dict[int, list[str]]) -> None:
         """mfmas: ("qk", stage, half, c, S) or ("pv", stage, st16, dt, P).
         fill[i]: instructions emitted right after MFMA i.  The LDS operands of MFMA i
         go to slot i % NSLOT and are read LA MFMAs ahead."""
+        L = self.L
         n = len(mfmas)
         LA = self.la
         nreads = [1 if (m[0] == "qk" or self.pv_b128) else 2 for m in mfmas]
 
         def reads(i: int) -> list[str]:
             m = mfmas[i]
-            slot = OPS + 4 * (i % NSLOT)
+            slot = L.OPS + 4 * (i % NSLOT)
             if m[0] == "qk":
                 _, st, half, c, _ = m
-                return [f"ds_read_b128 {vr(slot, 4)}, {vr(KOFF + c)} offset:{st * TILE + half * 8192}"]
+                return [f"ds_read_b128 {vr(slot, 4)}, {vr(L.KOFF + c)} offset:{st * L.TILE + half * 32 * L.RB}"]
             _, st, st16, dt, _ = m
-            off = st * TILE + st16 * 4096    # the V^T read offsets include VBASE
+            off = st * L.TILE + st16 * 16 * L.RB    # the V^T read offsets include VBASE
             if self.pv_b128:
-                return [f"ds_read_b128 {vr(slot, 4)}, {vr(KOFF + dt)} offset:{off}"]
-            return [f"ds_read_b64_tr_b16 {vr(slot, 2)}, {vr(VOFFA + dt)} offset:{off}",
-                    f"ds_read_b64_tr_b16 {vr(slot + 2, 2)}, {vr(VOFFB + dt)} offset:{off}"]
+                return [f"ds_read_b128 {vr(slot, 4)}, {vr(L.KOFF + dt)} offset:{off}"]
+            return [f"ds_read_b64_tr_b16 {vr(slot, 2)}, {vr(L.VOFFA + dt)} offset:{off}",
+                    f"ds_read_b64_tr_b16 {vr(slot + 2, 2)}, {vr(L.VOFFB + dt)} offset:{off}"]
 
         issued = min(LA, n)
         for i in range(issued):
@@ -304,13 +349,13 @@ class Gen:
             pending = sum(nreads[j] for j in range(i + 1, issued))
             self.e(f"s_waitcnt lgkmcnt({min(15, pending)})")
             m = mfmas[i]
-            slot = OPS + 4 * (i % NSLOT)
+            slot = L.OPS + 4 * (i % NSLOT)
             if m[0] == "qk":
                 _, _, _, c, S = m
-                self.e(f"{self.mfma} {vr(S, 16)}, {vr(slot, 4)}, {vr(Q + 4 * c, 4)}, {'0' if c == 0 else vr(S, 16)}")
+                self.e(f"{self.mfma} {vr(S, 16)}, {vr(slot, 4)}, {vr(L.Q + 4 * c, 4)}, {'0' if c == 0 else vr(S, 16)}")
             else:
                 _, _, st16, dt, P = m
-                acc = vr(O + 16 * dt, 16)
+                acc = vr(L.O + 16 * dt, 16)
                 self.e(f"{self.mfma} {acc}, {vr(slot, 4)}, {vr(P + 4 * (st16 & 1), 4)}, {acc}")
             if self.pad:
                 self.e("s_nop 15")
@@ -335,55 +380,63 @@ class Gen:
     def iteration(self, stage: int) -> None:
         """Block j: QK of its two sub-blocks (K in `stage`), softmax of sub-blocks
         2j-1 and 2j, PV of block j-1 (V in stage-1), copies of block j+2."""
+        L = self.L
         vst, cst = (stage + 3) & 3, (stage + 2) & 3
         site = f"I{stage}"
-        self.e(f"; ── block j, K stage {stage}", "s_waitcnt vmcnt(4)", "s_nop 0" if self.no_barrier else "s_barrier",
-               "s_waitcnt lgkmcnt(0)")
+        M = 2 * L.NQK                     # MFMAs per sub-iteration (QK and PV interleaved)
+        self.e(f"; ── block j, K stage {stage}", f"s_waitcnt vmcnt({2 * L.NCP})",
+               "s_nop 0" if self.no_barrier else "s_barrier", "s_waitcnt lgkmcnt(0)")
         mf = []
-        for half, S, P in ((0, SA, PA), (1, SB, PB)):
-            for c in range(8):
+        half_q = L.NQK // 2               # QK k-steps per 16-key PV step
+        for half, S, P in ((0, L.SA, L.PA), (1, L.SB, L.PB)):
+            for c in range(L.NQK):
                 mf.append(("qk", stage, half, c, S))
-                mf.append(("pv", vst, 2 * half + c // 4, c % 4, P))
+                mf.append(("pv", vst, 2 * half + c // half_q, c % L.NDT, P))
         fill: dict[int, list[str]] = {0: [] if self.no_decode else self.decode(S_ENT + 2 * cst, site)}
-        for k, at in enumerate((6, 10, 22, 26)):
+        at_copy = (6, 10, 22, 26) if L.NCP == 2 else (5, 13)
+        for k, at in enumerate(at_copy):
             fill.setdefault(at, []).extend(self.copy(cst, k))
         # sub-iteration a: softmax of sub-block 2j-1 (S_B, block j-1 half 1)
         fill.setdefault(1, []).extend(self.mask_check(site + "a", "B", S_ENT + 2 * vst + 1, 1))
-        self.spread(self.softmax_ops(SB, PB), list(range(2, 15)), fill)
-        fill.setdefault(15, []).extend(self.softmax_tail(site + "a", "B"))
+        self.spread(self.softmax_ops(L.SB, L.PB), list(range(2, M - 1)), fill)
+        fill.setdefault(M - 1, []).extend(self.softmax_tail(site + "a", "B"))
         # sub-iteration b: softmax of sub-block 2j (S_A, block j half 0)
-        fill.setdefault(17, []).extend(self.mask_check(site + "b", "A", S_ENT + 2 * stage + 1, 0))
-        self.spread(self.softmax_ops(SA, PA), list(range(18, 31)), fill)
-        fill.setdefault(31, []).extend(self.softmax_tail(site + "b", "A"))
+        fill.setdefault(M + 1, []).extend(self.mask_check(site + "b", "A", S_ENT + 2 * stage + 1, 0))
+        self.spread(self.softmax_ops(L.SA, L.PA), list(range(M + 2, 2 * M - 1)), fill)
+        fill.setdefault(2 * M - 1, []).extend(self.softmax_tail(site + "b", "A"))
         self.stream(mf, fill)
         self.iteration_tail(stage)
 
     def first_iteration(self) -> None:
         """Block 0: QK of its two sub-blocks, softmax of sub-block 0, copies of block 2."""
-        self.e("; ── block 0", "s_waitcnt vmcnt(4)", "s_barrier", "s_waitcnt lgkmcnt(0)")
-        mf = [("qk", 0, 0, c, SA) for c in range(8)] + [("qk", 0, 1, c, SB) for c in range(8)]
+        L = self.L
+        self.e("; ── block 0", f"s_waitcnt vmcnt({2 * L.NCP})", "s_barrier", "s_waitcnt lgkmcnt(0)")
+        mf = [("qk", 0, 0, c, L.SA) for c in range(L.NQK)] + [("qk", 0, 1, c, L.SB) for c in range(L.NQK)]
         fill: dict[int, list[str]] = {0: self.decode(S_ENT + 4, "F")}
-        for k in range(4):
+        for k in range(2 * L.NCP):
             fill.setdefault(1 + k, []).extend(self.copy(2, k))
-        fill.setdefault(9, []).extend(self.mask_check("F", "A", S_ENT + 1, 0))
-        self.spread(self.softmax_ops(SA, PA), list(range(10, 15)), fill)
-        fill.setdefault(15, []).extend(self.softmax_tail("F", "A"))
+        fill.setdefault(L.NQK + 1, []).extend(self.mask_check("F", "A", S_ENT + 1, 0))
+        self.spread(self.softmax_ops(L.SA, L.PA), list(range(L.NQK + 2, 2 * L.NQK - 1)), fill)
+        fill.setdefault(2 * L.NQK - 1, []).extend(self.softmax_tail("F", "A"))
         self.stream(mf, fill)
         self.iteration_tail(0)
 
     def drain(self, stage: int) -> None:
         """After block n-1 (in `stage`): softmax of sub-block 2n-1, PV of block n-1."""
+        L = self.L
         self.e(f"{lbl(f'DRAIN{stage}')}:")
-        mf = [("pv", stage, k // 4, k % 4, PA) for k in range(8)] + \
-             [("pv", stage, 2 + k // 4, k % 4, PB) for k in range(8)]
+        nh = L.NQK                        # PV MFMAs per half: 2 16-key steps x NDT d-tiles
+        mf = [("pv", stage, k // L.NDT, k % L.NDT, L.PA) for k in range(nh)] + \
+             [("pv", stage, 2 + k // L.NDT, k % L.NDT, L.PB) for k in range(nh)]
         fill: dict[int, list[str]] = {0: self.mask_check(f"D{stage}", "B", S_ENT + 2 * stage + 1, 1)}
-        self.spread(self.softmax_ops(SB, PB), list(range(1, 7)), fill)
-        fill.setdefault(7, []).extend(self.softmax_tail(f"D{stage}", "B"))
+        self.spread(self.softmax_ops(L.SB, L.PB), list(range(1, nh - 1)), fill)
+        fill.setdefault(nh - 1, []).extend(self.softmax_tail(f"D{stage}", "B"))
         self.stream(mf, fill)
         # the code after the asm reads O with VALU: 12 states after the last MFMA
         self.e("s_waitcnt vmcnt(0) lgkmcnt(0)", "s_nop 15", f"s_branch {lbl('END')}")
 
     def build(self) -> list[str]:
+        L = self.L
         e = self.e
         # setup: entries 0..2 (clamped to the last block), copies of blocks 0 and 1
         e(f"s_sub_u32 {sr(S_NM1)}, {sr(S_N)}, 1",
@@ -397,7 +450,7 @@ class Gen:
           "s_waitcnt lgkmcnt(0)")
         for blk in (0, 1):
             e(*self.decode(S_ENT + 2 * blk, f"S{blk}"))
-            for k in range(4):
+            for k in range(2 * L.NCP):
                 e(*self.copy(blk, k))
         self.first_iteration()
         e(f"{lbl('LOOP')}:")
@@ -407,33 +460,51 @@ class Gen:
         for stage in range(4):
             self.drain(stage)
         e(*self.stubs)
-        e(*self.rare_routine(SA, PA, "RARE_A"), *self.rare_routine(SB, PB, "RARE_B"), *self.switch_routine())
-        e(*self.mask_routine(SA, "MASK_A"), *self.mask_routine(SB, "MASK_B"))
+        e(*self.rare_routine(L.SA, L.PA, "RARE_A"), *self.rare_routine(L.SB, L.PB, "RARE_B"),
+          *self.switch_routine())
+        e(*self.mask_routine(L.SA, "MASK_A"), *self.mask_routine(L.SB, "MASK_B"))
         e(f"{lbl('END')}:")
         return self.lines
 
 
-def render(**opts) -> str:
-    out = ["// Generated by gen_stream_asm.py: the hand-scheduled key loop of",
-           "// attn_fwd_stream_kernel (lvsa_attn_stream.h).  Do not edit; regenerate.",
-           "#pragma once", ""]
-    for dt, name in (("bf16", "LVSA_STREAM_LOOP_BF16"), ("f16", "LVSA_STREAM_LOOP_F16")):
-        lines = Gen(dt, **opts).build()
-        out.append(f"#define {name} \\")
-        for ln in lines:
-            if not ln:
-                continue
-            if ln.startswith(";"):
-                continue
-            out.append(f'  "{ln}\\n" \\')
-        out.append('  ""')
-        out.append("")
-    clob = [f'"v{r}"' for r in CLOBBER_V] + [f'"s{r}"' for r in CLOBBER_S]
-    out.append("#define LVSA_STREAM_CLOBBERS \\")
+def operands(D: int) -> list[str]:
+    """Macros with the asm operand lists of the D kernel (outputs, inputs, clobbers)."""
+    L = Layout(D)
+    os_ = ", ".join(f"o{t}" for t in range(L.NDT))
+    outs = ", ".join(f'"+{{{vr(L.O + 16 * t, 16)}}}"(o{t})' for t in range(L.NDT))
+    outs += f', "+{{{vr(L.VM, 2)}}}"(ml), "+{{{vr(L.ROW, 4)}}}"(misc)'
+    ins = (f'"{{{vr(L.Q, 4 * L.NQK)}}}"(qv), "{{{vr(L.KOFF, L.NQK)}}}"(koff), '
+           f'"{{{vr(L.VOFFA, 2 * L.NDT)}}}"(voff), "{{{vr(L.DMAROW, 2)}}}"(dma), '
+           f'"{{s[20:23]}}"(sa), "{{s[24:31]}}"(sb), "{{s[32:39]}}"(sc)')
+    clob = [f'"v{r}"' for r in L.CLOBBER_V] + [f'"s{r}"' for r in CLOBBER_S]
+    out = [f"#define LVSA_STREAM{D}_OUTPUTS({os_}, ml, misc) {outs}",
+           f"#define LVSA_STREAM{D}_INPUTS(qv, koff, voff, dma, sa, sb, sc) {ins}",
+           f"#define LVSA_STREAM{D}_CLOBBERS \\"]
     for i in range(0, len(clob), 12):
         out.append("  " + ", ".join(clob[i:i + 12]) + ", \\")
     out.append('  "vcc", "m0", "scc", "memory"')
-    out.append("")
+    return out
+
+
+def render(**opts) -> str:
+    out = ["// Generated by gen_stream_asm.py: the hand-scheduled key loops of",
+           "// attn_fwd_stream_kernel (lvsa_attn_stream.h) and their asm operand lists.",
+           "// Do not edit; regenerate.",
+           "#pragma once", ""]
+    for D in (128, 64):
+        for dt, name in (("bf16", f"LVSA_STREAM{D}_LOOP_BF16"), ("f16", f"LVSA_STREAM{D}_LOOP_F16")):
+            lines = Gen(dt, D=D, **opts).build()
+            out.append(f"#define {name} \\")
+            for ln in lines:
+                if not ln:
+                    continue
+                if ln.startswith(";"):
+                    continue
+                out.append(f'  "{ln}\\n" \\')
+            out.append('  ""')
+            out.append("")
+        out += operands(D)
+        out.append("")
     return "\n".join(out)
 
 

@@ -225,7 +225,7 @@ extern "C" int lvsa_attn_fwd(const lvsa_attn_args* a, hipStream_t stream) {
   p.text_chunks = chunks;
   p.text_first = chunks == 1 ? 1 : 0;
   p.ws = chunks > 1 ? (float*)a->workspace : nullptr;
-  // The single-stream D = 128 kernel serves plans without generic descriptors:
+  // The single-stream kernel (D = 64 and 128) serves plans without generic descriptors:
   // 256-row tiles touch at most two query frames when frames have >= 255
   // rows, and 64-key blocks (even short last ones) at most two key frames
   // when frames have >= 64 keys.  LVSA_ATTN_KERNEL=pp selects the ping-pong
@@ -237,7 +237,7 @@ extern "C" int lvsa_attn_fwd(const lvsa_attn_args* a, hipStream_t stream) {
   auto fits32 = [](int64_t rows, int64_t row_elems) { return (rows + kBN) * row_elems * 2 < (1LL << 32); };
   const bool src32 = fits32(a->n_k, a->k_str[1]) && fits32(a->n_k, a->v_str[1]) &&
                      (a->n_x == 0 || (fits32(a->n_x, a->kx_str[1]) && fits32(a->n_x, a->vx_str[1])));
-  p.use_stream = (!fp32 && a->D == 128 && a->block_q == kPPBM && !force_pp && src32 &&
+  p.use_stream = (!fp32 && (a->D == 128 || a->D == 64) && a->block_q == kPPBM && !force_pp && src32 &&
                   (a->n_q == 0 || (p.R >= 255 && p.C >= 64))) ? 1 : 0;
   const int bq = a->block_q;
   const bool bf16 = a->dtype == LVSA_BF16;

@@ -585,8 +585,8 @@ def test_wrapper_rejects_out_of_range_columns(gpu):
 
 
 def _stream_cfg(seed):
-    """Random geometries the single-stream D = 128 kernel serves (frames of at
-    least 255 tokens): window / keyframe patterns, text, GQA, both dtypes."""
+    """Random geometries the single-stream kernel serves (frames of at least
+    255 tokens): window / keyframe patterns, text, GQA, both dtypes."""
     g = torch.Generator().manual_seed(2000 + seed)
     pick = lambda xs: xs[int(torch.randint(len(xs), (1,), generator=g))]  # noqa: E731
     T = int(torch.randint(1, 14, (1,), generator=g))
@@ -602,16 +602,17 @@ def _stream_cfg(seed):
     return T, P, W, n, kfi, off, H, Hkv, n_txt, dt
 
 
+@pytest.mark.parametrize("D", [128, 64])
 @pytest.mark.parametrize("seed", range(16))
-def test_stream_kernel_random_geometries(seed, gpu, monkeypatch):
-    """D = 128 on frames of >= 255 tokens runs the hand-scheduled single-stream
-    kernel; against the fp32 oracle, and the ping-pong kernel within bf16
-    rounding."""
+def test_stream_kernel_random_geometries(seed, D, gpu, monkeypatch):
+    """D = 64 and 128 on frames of >= 255 tokens run the hand-scheduled
+    single-stream kernel; against the fp32 oracle, and the ping-pong kernel
+    within bf16 rounding."""
     T, P, W, n, kfi, off, H, Hkv, n_txt, dt = _stream_cfg(seed)
     N = T * P
     m = _meta(T, P, W, n, kfi, off)
-    q, k, v, qt, kt, vt = _draw([(1, N, H, 128), (1, N, Hkv, 128), (1, N, Hkv, 128), (1, n_txt, H, 128),
-                                 (1, n_txt, Hkv, 128), (1, n_txt, Hkv, 128)], seed=seed, dtype=dt)
+    q, k, v, qt, kt, vt = _draw([(1, N, H, D), (1, N, Hkv, D), (1, N, Hkv, D), (1, n_txt, H, D),
+                                 (1, n_txt, Hkv, D), (1, n_txt, Hkv, D)], seed=seed, dtype=dt)
     rows = [set(r) for r in om.build_frame_mask(T, P, W, n, kfi, offset=off).rows]
     args = dict(k_text=kt.to(gpu), v_text=vt.to(gpu), q_text=qt.to(gpu)) if n_txt else {}
     res = lv.lvsa_attention(q.to(gpu), k.to(gpu), v.to(gpu), m, return_lse=True, **args)
@@ -619,7 +620,7 @@ def test_stream_kernel_random_geometries(seed, gpu, monkeypatch):
     res_pp = lv.lvsa_attention(q.to(gpu), k.to(gpu), v.to(gpu), m, return_lse=True, **args)
     ro, rl = oa.per_frame_sdpa(q.float(), k.float(), v.float(), rows, P,
                                k_extra=kt.float() if n_txt else None, v_extra=vt.float() if n_txt else None)
-    what = f"seed {seed}: T={T} P={P} W={W} n={n} kfi={kfi} off={off} H={H}/{Hkv} txt={n_txt} {dt}"
+    what = f"seed {seed}: D={D} T={T} P={P} W={W} n={n} kfi={kfi} off={off} H={H}/{Hkv} txt={n_txt} {dt}"
     o, lse = (res[0], res[2]) if n_txt else res
     _close(o, ro, what)
     torch.testing.assert_close(lse.cpu(), rl, atol=2e-2, rtol=0, msg=what)

@@ -1,4 +1,4 @@
-"""The hand-scheduled key loop of the single-stream D = 128 kernel, on the CPU.
+"""The hand-scheduled key loops of the single-stream kernel (D = 64, 128), on the CPU.
 
 * The committed lvsa_attn_stream_body.inc is what gen_stream_asm.py generates.
 * tests/asm_sim.py runs the generated loop for the 8 waves of one 256-row
@@ -24,8 +24,11 @@ def test_committed_loop_is_generated():
     assert (CSRC / "lvsa_attn_stream_body.inc").read_text() == A.G.render()
 
 
-def _swz(r):
-    return ((r & 3) << 2) | ((r >> 2) & 3)
+def _swz(r, D=128):
+    """16-byte chunk swizzle of LDS row r (lvsa_attn_kernels.h swz<D>)."""
+    if D == 128:
+        return ((r & 3) << 2) | ((r >> 2) & 3)
+    return (((r >> 1) & 1) << 2) | (((r >> 2) & 1) << 1) | ((r >> 3) & 1)
 
 
 def _desc_two_part(bits, kb, qs):
@@ -43,15 +46,19 @@ def _allowed(y, row, key_in_block):
     return bool((bits >> bit) & 1)
 
 
-def run_loop(entries, nk, n_x, seed=0, dt="bf16", **opts):
+def run_loop(entries, nk, n_x, seed=0, dt="bf16", D=128, **opts):
+    """Run the generated loop for the 8 waves of one work-group with the
+    registers the C++ prologue of attn_fwd_stream_kernel sets up."""
     rng = np.random.default_rng(seed)
-    D, R = 128, 256
+    R = 256
+    L = A.G.Layout(D)
+    RB, NCH = 2 * D, D // 8
     rnd = (lambda x: A.bf16_to_f32(A.bf16_round(x))) if dt == "bf16" else (lambda x: x.astype(np.float16).astype(np.float32))
     enc = (lambda x: A.bf16_round(x).astype(np.uint16).tobytes()) if dt == "bf16" else (lambda x: x.astype(np.float16).tobytes())
     q = rnd(rng.standard_normal((R, D)).astype(np.float32))
     k, v = (rnd(rng.standard_normal((nk, D)).astype(np.float32)) for _ in range(2))
     kx, vx = (rnd(rng.standard_normal((max(n_x, 1), D)).astype(np.float32)) for _ in range(2))
-    sim = A.Sim(dt, **opts)
+    sim = A.Sim(dt, D=D, **opts)
     kb0, vb0, kb1, vb1 = (sim.mem.alloc(enc(x)) for x in (k, v, kx, vx))
     ep = sim.mem.alloc(b"".join(struct.pack("<II", x, y) for x, y in entries))
     scale = 1 / math.sqrt(D)
@@ -63,31 +70,32 @@ def run_loop(entries, nk, n_x, seed=0, dt="bf16", **opts):
         W = A.Wave(w, sim)
         V = W.v
         rows = 32 * w + i32
-        for c in range(8):
+        for c in range(L.NQK):
             for j in range(4):
                 d0 = 16 * c + 8 * h + 2 * j
-                V[64 + 4 * c + j] = qbits[rows, d0] | (qbits[rows, d0 + 1] << 16)
-        sw = np.array([_swz(x & 15) for x in i32])
-        for c in range(8):
-            V[176 + c] = i32 * 256 + (((2 * c + h) ^ sw) << 4)
+                V[L.Q + 4 * c + j] = qbits[rows, d0] | (qbits[rows, d0 + 1] << 16)
+        sw = np.array([_swz(x & 15, D) for x in i32])
+        for c in range(L.NQK):
+            V[L.KOFF + c] = i32 * RB + (((2 * c + h) ^ sw) << 4)
         rowA = 4 * h + ((lane & 15) >> 2)
         dgrp = (lane >> 4) & 1
-        for dt_ in range(4):
+        for dt_ in range(L.NDT):
             chunk = 4 * dt_ + 2 * dgrp + ((lane & 3) >> 1)
             inb = (lane & 1) * 8
-            V[184 + dt_] = 65536 + rowA * 256 + ((chunk ^ np.array([_swz(x) for x in rowA])) << 4) + inb
-            V[188 + dt_] = 65536 + (rowA + 8) * 256 + ((chunk ^ np.array([_swz(x) for x in rowA + 8])) << 4) + inb
-        crow = 4 * w + lane // 16
-        V[196] = crow
-        V[197] = ((lane & 15) ^ np.array([_swz(x & 15) for x in crow])) * 16
-        V[200], V[201], V[202], V[203] = 32 * w + i32, 4 * h, 0xFF800000, 0
-        V[192] = A.f2u(np.full(64, -1e30, np.float32))
+            V[L.VOFFA + dt_] = L.VBASE + rowA * RB + ((chunk ^ np.array([_swz(x, D) for x in rowA])) << 4) + inb
+            V[L.VOFFB + dt_] = (L.VBASE + (rowA + 8) * RB +
+                                ((chunk ^ np.array([_swz(x, D) for x in rowA + 8])) << 4) + inb)
+        crow = w * (1024 // RB) + lane // NCH
+        V[L.DMAROW] = crow
+        V[L.C16] = ((lane % NCH) ^ np.array([_swz(x & 15, D) for x in crow])) * 16
+        V[L.ROW], V[L.H4], V[L.NEGINF], V[L.VT] = 32 * w + i32, 4 * h, 0xFF800000, 0
+        V[L.VM] = A.f2u(np.full(64, -1e30, np.float32))
         S = W.s
         S[20], S[21], S[22] = ep & 0xFFFFFFFF, ep >> 32, len(entries)
         S[23] = int(A.f2u(np.float32(scale * 1.4426950408889634)))
         for i, b in enumerate((kb0, vb0, kb1, vb1)):
             S[24 + 2 * i], S[25 + 2 * i] = b & 0xFFFFFFFF, b >> 32
-        S[32:36] = [256, 256, 256, 256]
+        S[32:36] = [RB, RB, RB, RB]
         S[36], S[37], S[38], S[39] = nk, n_x, w, 1024 * w
         waves.append(W)
     sim.run(waves)
@@ -96,11 +104,11 @@ def run_loop(entries, nk, n_x, seed=0, dt="bf16", **opts):
     for w, W in enumerate(waves):
         for ln in range(64):
             r, hh = 32 * w + (ln & 31), ln >> 5
-            for dt_ in range(4):
+            for dt_ in range(L.NDT):
                 for rr in range(16):
-                    O[r, 32 * dt_ + 8 * (rr // 4) + 4 * hh + rr % 4] = A.u2f(W.v[16 * dt_ + rr, ln])
-            lsum[r] += A.u2f(W.v[193, ln])
-            mrun[r] = A.u2f(W.v[192, ln])
+                    O[r, 32 * dt_ + 8 * (rr // 4) + 4 * hh + rr % 4] = A.u2f(W.v[L.O + 16 * dt_ + rr, ln])
+            lsum[r] += A.u2f(W.v[L.VL, ln])
+            mrun[r] = A.u2f(W.v[L.VM, ln])
     # reference: float64 softmax attention over the allowed keys
     ref = np.zeros((R, D))
     lse_ref = np.zeros(R)
@@ -136,23 +144,26 @@ CASES = {
 }
 
 
+@pytest.mark.parametrize("D", [128, 64])
 @pytest.mark.parametrize("case", sorted(CASES))
-def test_loop_matches_attention(case):
+def test_loop_matches_attention(case, D):
     make, nk, n_x = CASES[case]
     entries = make()
-    err, lse_err, copies = run_loop(entries, nk, n_x)
+    err, lse_err, copies = run_loop(entries, nk, n_x, D=D)
     assert err <= 4e-3 and lse_err <= 2e-3, (case, err, lse_err)
-    # 4 copies per wave per block for blocks 0..n+1 (the last two repeat block n-1)
-    assert copies == 8 * 4 * (len(entries) + 2)
+    # D/32 copies per wave per block for blocks 0..n+1 (the last two repeat block n-1)
+    assert copies == 8 * (D // 32) * (len(entries) + 2)
 
 
-def test_loop_rare_path_every_sub_block():
+@pytest.mark.parametrize("D", [128, 64])
+def test_loop_rare_path_every_sub_block(D):
     """The exact-max path (rescale of O and l) on every sub-block gives the
     same attention."""
-    err, lse_err, _ = run_loop([(j, 0) for j in range(3)], 192, 0, seed=3, always_rare=True)
+    err, lse_err, _ = run_loop([(j, 0) for j in range(3)], 192, 0, seed=3, D=D, always_rare=True)
     assert err <= 4e-3 and lse_err <= 2e-3
 
 
-def test_loop_fp16():
-    err, lse_err, _ = run_loop([(j, _tail(150, j)) for j in range(3)], 150, 0, seed=4, dt="f16")
+@pytest.mark.parametrize("D", [128, 64])
+def test_loop_fp16(D):
+    err, lse_err, _ = run_loop([(j, _tail(150, j)) for j in range(3)], 150, 0, seed=4, dt="f16", D=D)
     assert err <= 2e-3 and lse_err <= 2e-3
