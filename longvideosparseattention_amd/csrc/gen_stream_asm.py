@@ -117,7 +117,8 @@ def lbl(name: str) -> str:
 class Gen:
     def __init__(self, dt: str, D: int = 128, pad: bool = False, always_rare: bool = False, la: int = LA,
                  pv_b128: bool = False, no_softmax: bool = False, order: str = "group",
-                 no_barrier: bool = False, no_decode: bool = False, no_exp: bool = False):
+                 no_barrier: bool = False, no_decode: bool = False, no_exp: bool = False,
+                 lead: int = 0, early_load: bool = False, no_mask: bool = False):
         assert dt in ("bf16", "f16")
         self.dt = dt
         self.L = Layout(D)
@@ -130,6 +131,9 @@ class Gen:
         self.no_barrier = no_barrier    # timing only (wrong results): no work-group barrier
         self.no_decode = no_decode      # timing only (wrong results): copy sources not updated
         self.no_exp = no_exp            # timing only (wrong results): no exponentials
+        self.lead = lead                # PV MFMAs that open a block, their V operands read before the barrier
+        self.early_load = early_load    # plan entry j+3 loaded in the middle of block j, not after it
+        self.no_mask = no_mask          # timing only (wrong results): masks not applied
         self.lines: list[str] = []
         self.stubs: list[str] = []
 
@@ -192,6 +196,8 @@ class Gen:
                 f"v_add_f32 {vr(L.VL)}, {vr(L.VL)}, {vr(L.LS0)}"]
 
     def mask_check(self, site: str, sset: str, desc: int, half: int) -> list[str]:
+        if self.no_mask:
+            return []
         self.stubs += [f"{lbl('MSTUB_' + site)}:", f"s_mov_b32 s91, {sr(desc)}", f"s_mov_b32 s75, {32 * half}",
                        f"s_call_b64 {sr(S_RET, 2)}, {lbl('MASK_' + sset)}", f"s_branch {lbl('MRET_' + site)}"]
         return [f"s_and_b32 s74, {sr(desc)}, 3", "s_cmp_lg_u32 s74, 0", f"s_cbranch_scc1 {lbl('MSTUB_' + site)}",
@@ -320,17 +326,21 @@ class Gen:
                 f"buffer_load_dwordx4 {vr(L.DV if v else L.DK)}, {sr(rs, 4)}, {so} offen lds"]
 
     # ── an MFMA stream with its operand reads and the interleaved work ──
-    def stream(self, mfmas: list[tuple], fill: dict[int, list[str]]) -> None:
+    def stream(self, mfmas: list[tuple], fill: dict[int, list[str]], pre: int = 0,
+               nxt: list[tuple] = ()) -> None:
         """mfmas: ("qk", stage, half, c, S) or ("pv", stage, st16, dt, P).
         fill[i]: instructions emitted right after MFMA i.  The LDS operands of MFMA i
-        go to slot i % NSLOT and are read LA MFMAs ahead."""
+        go to slot i % NSLOT and are read LA MFMAs ahead.  The operands of the first
+        `pre` MFMAs were read by the previous stream; `nxt` are the first MFMAs of the
+        next stream, whose operands this one reads as if they followed it."""
         L = self.L
-        n = len(mfmas)
+        seq = list(mfmas) + list(nxt)
+        n, nn = len(mfmas), len(seq)
         LA = self.la
-        nreads = [1 if (m[0] == "qk" or self.pv_b128) else 2 for m in mfmas]
+        nreads = [1 if (m[0] == "qk" or self.pv_b128) else 2 for m in seq]
 
         def reads(i: int) -> list[str]:
-            m = mfmas[i]
+            m = seq[i]
             slot = L.OPS + 4 * (i % NSLOT)
             if m[0] == "qk":
                 _, st, half, c, _ = m
@@ -342,11 +352,11 @@ class Gen:
             return [f"ds_read_b64_tr_b16 {vr(slot, 2)}, {vr(L.VOFFA + dt)} offset:{off}",
                     f"ds_read_b64_tr_b16 {vr(slot + 2, 2)}, {vr(L.VOFFB + dt)} offset:{off}"]
 
-        issued = min(LA, n)
-        for i in range(issued):
+        issued = min(LA + pre, n)
+        for i in range(pre, issued):
             self.e(*reads(i))
         for i in range(n):
-            pending = sum(nreads[j] for j in range(i + 1, issued))
+            pending = sum(nreads[j] for j in range(max(i + 1, pre), issued))
             self.e(f"s_waitcnt lgkmcnt({min(15, pending)})")
             m = mfmas[i]
             slot = L.OPS + 4 * (i % NSLOT)
@@ -359,10 +369,13 @@ class Gen:
                 self.e(f"{self.mfma} {acc}, {vr(slot, 4)}, {vr(P + 4 * (st16 & 1), 4)}, {acc}")
             if self.pad:
                 self.e("s_nop 15")
-            if issued < n:
+            while issued < min(nn, i + 1 + LA):
                 self.e(*reads(issued))
                 issued += 1
             self.e(*fill.get(i, []))
+        while issued < nn:                # the next stream's operands not yet read
+            self.e(*reads(issued))
+            issued += 1
 
     @staticmethod
     def spread(ops: list[str], slots: list[int], fill: dict[int, list[str]]) -> None:
@@ -370,12 +383,23 @@ class Gen:
         for i, s in enumerate(slots):
             fill.setdefault(s, []).extend(ops[i * per:(i + 1) * per])
 
-    def iteration_tail(self, stage: int) -> None:
-        """Scalar load of entry j+3, j += 1, leave for the drain after the last block."""
-        self.e(f"s_add_u32 s74, {sr(S_J)}, 3", f"s_min_u32 s74, s74, {sr(S_NM1)}", "s_lshl_b32 s74, s74, 3",
-               f"s_load_dwordx2 {sr(S_ENT + 2 * ((stage + 3) & 3), 2)}, {sr(S_EPTR, 2)}, s74",
-               f"s_add_u32 {sr(S_J)}, {sr(S_J)}, 1", f"s_cmp_ge_u32 {sr(S_J)}, {sr(S_N)}",
+    def entry_load(self, stage: int) -> list[str]:
+        """Scalar load of entry j+3 (clamped to the last) into the ring slot of entry j-1."""
+        return [f"s_add_u32 s74, {sr(S_J)}, 3", f"s_min_u32 s74, s74, {sr(S_NM1)}", "s_lshl_b32 s74, s74, 3",
+                f"s_load_dwordx2 {sr(S_ENT + 2 * ((stage + 3) & 3), 2)}, {sr(S_EPTR, 2)}, s74"]
+
+    def iteration_tail(self, stage: int, load: bool = True) -> None:
+        """Scalar load of entry j+3 (unless issued earlier), j += 1, leave for the
+        drain after the last block."""
+        if load:
+            self.e(*self.entry_load(stage))
+        self.e(f"s_add_u32 {sr(S_J)}, {sr(S_J)}, 1", f"s_cmp_ge_u32 {sr(S_J)}, {sr(S_N)}",
                f"s_cbranch_scc1 {lbl(f'DRAIN{stage}')}")
+
+    def lead_pv(self, stage: int) -> list[tuple]:
+        """The PV MFMAs that open the block after the one in `stage` (V of that block,
+        first 16 keys): their operands are read before the barrier."""
+        return [("pv", stage, 0, dt, self.L.PA) for dt in range(min(self.lead, self.L.NDT))]
 
     def iteration(self, stage: int) -> None:
         """Block j: QK of its two sub-blocks (K in `stage`), softmax of sub-blocks
@@ -389,9 +413,15 @@ class Gen:
         mf = []
         half_q = L.NQK // 2               # QK k-steps per 16-key PV step
         for half, S, P in ((0, L.SA, L.PA), (1, L.SB, L.PB)):
+            qks = [("qk", stage, half, c, S) for c in range(L.NQK)]
+            pvs = [("pv", vst, 2 * half + c // half_q, c % L.NDT, P) for c in range(L.NQK)]
+            lead = len(self.lead_pv(vst)) if half == 0 else 0
+            mf += pvs[:lead]
             for c in range(L.NQK):
-                mf.append(("qk", stage, half, c, S))
-                mf.append(("pv", vst, 2 * half + c // half_q, c % L.NDT, P))
+                mf.append(qks[c])
+                if lead + c < L.NQK:
+                    mf.append(pvs[lead + c])
+        assert mf[:len(self.lead_pv(vst))] == self.lead_pv(vst)
         fill: dict[int, list[str]] = {0: [] if self.no_decode else self.decode(S_ENT + 2 * cst, site)}
         at_copy = (6, 10, 22, 26) if L.NCP == 2 else (5, 13)
         for k, at in enumerate(at_copy):
@@ -402,10 +432,13 @@ class Gen:
         fill.setdefault(M - 1, []).extend(self.softmax_tail(site + "a", "B"))
         # sub-iteration b: softmax of sub-block 2j (S_A, block j half 0)
         fill.setdefault(M + 1, []).extend(self.mask_check(site + "b", "A", S_ENT + 2 * stage + 1, 0))
+        if self.early_load:
+            fill.setdefault(M, []).extend(self.entry_load(stage))
         self.spread(self.softmax_ops(L.SA, L.PA), list(range(M + 2, 2 * M - 1)), fill)
         fill.setdefault(2 * M - 1, []).extend(self.softmax_tail(site + "b", "A"))
-        self.stream(mf, fill)
-        self.iteration_tail(stage)
+        lead = self.lead_pv(vst)
+        self.stream(mf, fill, pre=len(lead), nxt=self.lead_pv(stage))
+        self.iteration_tail(stage, load=not self.early_load)
 
     def first_iteration(self) -> None:
         """Block 0: QK of its two sub-blocks, softmax of sub-block 0, copies of block 2."""
@@ -418,7 +451,7 @@ class Gen:
         fill.setdefault(L.NQK + 1, []).extend(self.mask_check("F", "A", S_ENT + 1, 0))
         self.spread(self.softmax_ops(L.SA, L.PA), list(range(L.NQK + 2, 2 * L.NQK - 1)), fill)
         fill.setdefault(2 * L.NQK - 1, []).extend(self.softmax_tail("F", "A"))
-        self.stream(mf, fill)
+        self.stream(mf, fill, nxt=self.lead_pv(0))
         self.iteration_tail(0)
 
     def drain(self, stage: int) -> None:

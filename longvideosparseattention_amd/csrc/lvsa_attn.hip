@@ -32,6 +32,32 @@ int64_t text_ws_bytes(const lvsa_attn_args* a, int chunks) {
   return 4 * (text_ws_o_elems(chunks, a->B, a->H, a->n_tq, a->D) + 2LL * chunks * a->B * a->H * a->n_tq);
 }
 
+// Workspace of a call: the text-split partials (text_ws_bytes) at offset 0,
+// then the work-queue counters (kQueueBytes) at a 256-byte boundary.
+int64_t queue_offset(int64_t text_bytes) { return (text_bytes + 255) & ~int64_t(255); }
+int64_t ws_bytes(const lvsa_attn_args* a) { return queue_offset(text_ws_bytes(a, text_chunks_of(a))) + kQueueBytes; }
+
+// Zero the work-queue counters (a kernel, not a memset, so the call can be
+// captured in a HIP graph and replayed).
+__global__ __launch_bounds__(64) void queue_reset_kernel(uint32_t* q) {
+  if (threadIdx.x < 8) q[threadIdx.x * (kQueueStride / 4)] = 0u;
+}
+
+// Compute units of the current device (the persistent grid of the
+// single-stream kernel), cached per device.
+int cu_count() {
+  static std::mutex mu;
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  std::lock_guard<std::mutex> lock(mu);
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0) cached[dev] = n;
+  }
+  return cached[dev];
+}
+
 // Exact log-sum-exp merge of the text chunks (lvsa-vllm-omni/lvsa_vllm_omni/
 // flashinfer_runner.py:184-197 merges two key sets the same way): with m_c the
 // running max (log2 units), l_c the row sum and o_c the unnormalised O of
@@ -166,7 +192,7 @@ extern "C" int lvsa_attn_fwd(const lvsa_attn_args* a, hipStream_t stream) {
                  (long long)first, (long long)last, a->rel_rows);
   }
   const int chunks = a->workspace ? text_chunks_of(a) : 1;
-  const int64_t ws_need = text_ws_bytes(a, chunks);
+  const int64_t ws_need = a->workspace ? ws_bytes(a) : 0;
   LVSA_REQUIRE(a->workspace_bytes >= ws_need, LVSA_ERR_CAPACITY,
                "lvsa_attn_fwd: workspace of %lld bytes < %lld needed (lvsa_attn_workspace_query)",
                (long long)a->workspace_bytes, (long long)ws_need);
@@ -239,6 +265,18 @@ extern "C" int lvsa_attn_fwd(const lvsa_attn_args* a, hipStream_t stream) {
                      (a->n_x == 0 || (fits32(a->n_x, a->kx_str[1]) && fits32(a->n_x, a->vx_str[1])));
   p.use_stream = (!fp32 && (a->D == 128 || a->D == 64) && a->block_q == kPPBM && !force_pp && src32 &&
                   (a->n_q == 0 || (p.R >= 255 && p.C >= 64))) ? 1 : 0;
+  // With a workspace, the single-stream kernel runs one persistent
+  // work-group per CU over the work queues (counters zeroed first).
+  p.queues = nullptr;
+  p.grid = (int)work;
+  const int cus = cu_count();
+  if (p.use_stream && a->workspace && cus > 0 && work > cus) {
+    p.queues = (uint32_t*)((char*)a->workspace + queue_offset(text_ws_bytes(a, chunks)));
+    p.grid = cus;
+    hipLaunchKernelGGL(queue_reset_kernel, dim3(1), dim3(64), 0, stream, p.queues);
+    const int qrc = launch_status("lvsa_attn_fwd (queue reset)");
+    if (qrc != LVSA_OK) return qrc;
+  }
   const int bq = a->block_q;
   const bool bf16 = a->dtype == LVSA_BF16;
   int rc;
@@ -270,7 +308,7 @@ extern "C" int lvsa_attn_workspace_query(const lvsa_attn_args* a, int64_t* bytes
                "lvsa_attn_workspace_query: bad sizes");
   LVSA_REQUIRE(a->D == 64 || a->D == 96 || a->D == 128 || a->D == 192 || a->D == 256, LVSA_ERR_UNSUPPORTED,
                "lvsa_attn_workspace_query: head_dim %d not supported", a->D);
-  *bytes = text_ws_bytes(a, text_chunks_of(a));
+  *bytes = ws_bytes(a);
   return LVSA_OK;
 }
 

@@ -9,10 +9,10 @@ namespace lvsa {
 int launch_d64(const AttnParams& prm, int block_q, bool bf16, hipStream_t stream) {
   if (block_q == kPPBM && prm.use_stream) {
     if (bf16) {
-      hipLaunchKernelGGL((attn_fwd_stream_kernel<64, __bf16>), dim3(prm.total_work), dim3(kPPThreads), 0, stream,
+      hipLaunchKernelGGL((attn_fwd_stream_kernel<64, __bf16>), dim3(prm.grid), dim3(kPPThreads), 0, stream,
                          prm);
     } else {
-      hipLaunchKernelGGL((attn_fwd_stream_kernel<64, _Float16>), dim3(prm.total_work), dim3(kPPThreads), 0,
+      hipLaunchKernelGGL((attn_fwd_stream_kernel<64, _Float16>), dim3(prm.grid), dim3(kPPThreads), 0,
                          stream, prm);
     }
     return launch_status("lvsa_attn_fwd");

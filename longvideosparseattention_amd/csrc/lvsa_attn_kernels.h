@@ -72,7 +72,17 @@ struct AttnParams {
   // descriptors "none" and "two-part", which is all such a plan holds when
   // query frames span at least 255 rows and key frames at least 64)
   int use_stream;
+  // Work queues (single-stream kernel with a workspace): `grid` persistent
+  // work-groups, one per CU, take work items from 8 queues, one per XCD,
+  // whose counters (kQueueStride bytes apart, zeroed before the launch) are
+  // at `queues`; null: one work-group per item, mapped by map_work.
+  uint32_t* queues;
+  int grid;
 };
+
+// Bytes of the work-queue counters at the end of the attention workspace.
+constexpr int kQueueStride = 128;                  // one counter per 128-byte line
+constexpr int64_t kQueueBytes = 8 * kQueueStride;
 
 // Layout of the text-split scratch: O partials [chunk][B][H][n_tq][D] fp32,
 // then (running max in log2 units, row sum) pairs [chunk][B][H][n_tq].
@@ -255,6 +265,76 @@ __device__ __forceinline__ WorkItem map_work(const AttnParams& p) {
   it.text = false;
   return it;
 }
+
+// Work queues.  Queue x (one per XCD) holds, in this order: the unsplit text
+// items t = x, x + 8, ... (the longest, first), the video items of the same
+// XCD-contiguous range map_work gives XCD x (consecutive tiles of a head, so
+// the K/V blocks they share stay in that XCD's L2), and the split text chunks
+// t = x, x + 8, ... (the shortest, last).  A work-group takes items from the
+// queue of its own XCD and, once that is empty, from the next ones in turn:
+// XCDs that run faster take over the items of the slower ones at the end, so
+// the launch does not wait for the slowest XCD's fixed share.
+struct QueueShape {
+  int n_first, v0, n_video, n_last;
+};
+__host__ __device__ inline QueueShape queue_shape(const AttnParams& p, int x) {
+  QueueShape q;
+  const int first = p.text_first ? p.n_twork : 0, last = p.text_first ? 0 : p.n_twork;
+  q.n_first = (first - x + kXcds - 1) / kXcds;   // items x, x + 8, ... below `first` (x < 8)
+  q.n_last = (last - x + kXcds - 1) / kXcds;
+  const int per = p.n_vwork / kXcds, rem = p.n_vwork % kXcds;
+  q.v0 = x * per + (x < rem ? x : rem);
+  q.n_video = per + (x < rem ? 1 : 0);
+  return q;
+}
+
+__host__ __device__ inline WorkItem text_item(const AttnParams& p, int t) {
+  WorkItem it;
+  it.chunk = t % p.text_chunks;
+  t /= p.text_chunks;
+  it.tile = p.n_vt + t % p.n_tt;
+  t /= p.n_tt;
+  it.head = t % p.H;
+  it.batch = t / p.H;
+  it.text = true;
+  return it;
+}
+
+// Item j of queue x.
+__host__ __device__ inline WorkItem queue_item(const AttnParams& p, int x, int j) {
+  const QueueShape q = queue_shape(p, x);
+  if (j < q.n_first) return text_item(p, x + kXcds * j);
+  j -= q.n_first;
+  if (j >= q.n_video) return text_item(p, x + kXcds * (j - q.n_video));
+  WorkItem it;
+  const int w = q.v0 + j;
+  it.tile = w % p.n_vt;
+  const int rest = w / p.n_vt;
+  it.head = rest % p.H;
+  it.batch = rest / p.H;
+  it.chunk = 0;
+  it.text = false;
+  return it;
+}
+
+// Next item for the calling work-group (one thread calls it): (j << 3) | x
+// for item j of queue x, or -1 once every queue is empty.  `x` is the queue
+// being drained and `dry` counts the queues found empty; counters only grow,
+// so a queue found empty is not visited again and a work-group gives up after
+// at most 8 failed increments.
+__device__ __forceinline__ int queue_next(const AttnParams& p, int& x, int& dry) {
+  while (dry < kXcds) {
+    const QueueShape q = queue_shape(p, x);
+    const uint32_t j = atomicAdd(p.queues + x * (kQueueStride / 4), 1u);
+    if (j < (uint32_t)(q.n_first + q.n_video + q.n_last)) return (int)(j << 3) | x;
+    x = (x + 1) & (kXcds - 1);
+    ++dry;
+  }
+  return -1;
+}
+
+// XCD of the calling wave (hardware register XCC_ID, bits 3:0).
+__device__ __forceinline__ int xcd_id() { return __builtin_amdgcn_s_getreg((3 << 11) | 20) & (kXcds - 1); }
 
 // Epilogue of a text chunk: the unnormalised O row of this lane (d = 32*dt +
 // 8*rq + 4*h .. +3 in oacc[dt][4*rq ..]) to `wo` (fp32), and the (running

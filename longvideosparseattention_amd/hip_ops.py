@@ -353,14 +353,16 @@ def attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, plan: BlockPlan,
              kx: Optional[torch.Tensor] = None, vx: Optional[torch.Tensor] = None,
              qt: Optional[torch.Tensor] = None, scale: Optional[float] = None,
              return_lse: bool = False, out: Optional[torch.Tensor] = None,
-             out_t: Optional[torch.Tensor] = None, text_split: bool = True
+             out_t: Optional[torch.Tensor] = None, scratch: bool = True
              ) -> Tuple[torch.Tensor, Optional[torch.Tensor], Optional[torch.Tensor], Optional[torch.Tensor]]:
     """Block-sparse attention over ``plan``: returns ``(o, o_text, lse, lse_text)``.
 
     ``lse`` is the natural-log log-sum-exp ``[B, H, S]`` (fp32) when requested.
-    ``text_split`` passes the scratch that lets long text-query tiles run as
-    key-range chunks merged by log-sum-exp (the default); ``False`` runs each
-    text tile as one work-group.
+    ``scratch`` (the default) passes the call's device scratch: the counters of
+    the work queues that balance the single-stream kernel's work-groups over
+    the XCDs, and the partials that let long text-query tiles run as key-range
+    chunks merged by log-sum-exp.  ``False`` launches one work-group per work
+    item and runs each text tile whole.
     """
     call = attn_args(q, k, v, plan, kx=kx, vx=vx, qt=qt, scale=scale, return_lse=return_lse, out=out,
                      out_t=out_t)
@@ -368,8 +370,8 @@ def attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, plan: BlockPlan,
     ws_bytes = C.c_int64(0)
     capi.check("lvsa_attn_workspace_query", capi.lib().lvsa_attn_workspace_query(C.byref(a), C.byref(ws_bytes)))
     ws = None
-    if ws_bytes.value > 0 and text_split:
-        # text-tile split scratch: partial O / (max, sum) per chunk, merged in the same call
+    if ws_bytes.value > 0 and scratch:
+        # work-queue counters (zeroed by the call) and the text-split partials
         ws = torch.empty(ws_bytes.value, dtype=torch.uint8, device=call.out.device)
         a.workspace, a.workspace_bytes = ws.data_ptr(), ws_bytes.value
     with torch.cuda.device(call.out.device):

@@ -158,12 +158,14 @@ def test_attn_workspace_query_and_capacity():
     assert lib.lvsa_attn_workspace_query(C.byref(a), C.byref(n)) == 0
     chunks = -(-(-(-20000 // 64)) // 128)           # 313 key blocks in chunks of 128
     assert chunks == 3
-    assert n.value == 4 * chunks * 2 * 100 * (128 + 2)
+    text = 4 * chunks * 2 * 100 * (128 + 2)          # partial O and (max, sum) per chunk
+    queues = 8 * 128                                  # one work-queue counter per 128-byte line
+    assert n.value == -(-text // 256) * 256 + queues
     a.workspace, a.workspace_bytes = 4096, n.value - 16
     assert lib.lvsa_attn_fwd(C.byref(a), None) == -3
     assert b"workspace" in lib.lvsa_last_error()
-    b = _attn_args(n_q=1000, rel_rows=10)     # no text queries: no scratch
-    assert lib.lvsa_attn_workspace_query(C.byref(b), C.byref(n)) == 0 and n.value == 0
+    b = _attn_args(n_q=1000, rel_rows=10)     # no text queries: the queue counters only
+    assert lib.lvsa_attn_workspace_query(C.byref(b), C.byref(n)) == 0 and n.value == queues
 
 
 def test_plan_rejects_query_rows_outside_relation():

@@ -533,7 +533,7 @@ def test_text_split_parity(cfg, gpu):
     plan = m.full_plan(gpu, N, N, n_txt, n_txt, D)
     o1, ot1, l1, lt1 = hip_ops.attn_fwd(g[0], g[1], g[2], plan, kx=g[4], vx=g[5], qt=g[3], return_lse=True)
     o0, ot0, l0, lt0 = hip_ops.attn_fwd(g[0], g[1], g[2], plan, kx=g[4], vx=g[5], qt=g[3], return_lse=True,
-                                        text_split=False)
+                                        scratch=False)
     assert torch.equal(o1, o0) and torch.equal(l1, l0)   # video rows do not depend on the split
     for b in range(B):
         rto, rtl = oa.text_row_attention(qt[b:b + 1].float(), k[b:b + 1].float(), v[b:b + 1].float(),
@@ -542,6 +542,45 @@ def test_text_split_parity(cfg, gpu):
         _close(ot0[b:b + 1], rto, f"unsplit text rows, batch {b}")
         torch.testing.assert_close(lt1[b:b + 1].cpu(), rtl, atol=2e-2, rtol=0)
     _close(ot1, ot0.float(), "split vs unsplit", max_abs=8e-3, mean_abs=5e-4)
+
+
+QUEUED = [
+    # T, P, H, Hkv, D, n_txt, B   (well over 256 work items: the persistent work-queue launch)
+    (24, 1100, 8, 2, 128, 300, 2),   # 1664 video tiles + split text chunks, GQA, batch 2
+    (13, 1350, 24, 24, 64, 226, 1),  # CogVideoX frame size and text length, half the heads
+    (40, 1560, 12, 12, 128, 0, 1),   # Wan frame size, video only
+]
+
+
+@pytest.mark.parametrize("cfg", QUEUED, ids=[str(c) for c in QUEUED])
+def test_work_queues_match_static_grid(cfg, gpu):
+    """The single-stream kernel over the work queues (one persistent
+    work-group per CU, items stolen across XCDs) computes every item exactly
+    as the launch with one work-group per item: video rows and LSE bit for
+    bit (the text rows differ only by the split), spot frames against the
+    fp32 oracle."""
+    T, P, H, Hkv, D, n_txt, B = cfg
+    N = T * P
+    m = _meta(T, P, 2, 1, 8, 3)
+    q, k, v, qt, kt, vt = _draw([(B, N, H, D), (B, N, Hkv, D), (B, N, Hkv, D), (B, n_txt, H, D),
+                                 (B, n_txt, Hkv, D), (B, n_txt, Hkv, D)], seed=21)
+    g = [x.to(gpu) for x in (q, k, v, qt, kt, vt)]
+    plan = m.full_plan(gpu, N, N, n_txt, n_txt, D)
+    kw = dict(kx=g[4], vx=g[5], qt=g[3]) if n_txt else {}
+    o1, ot1, l1, lt1 = hip_ops.attn_fwd(g[0], g[1], g[2], plan, return_lse=True, **kw)
+    o0, ot0, l0, lt0 = hip_ops.attn_fwd(g[0], g[1], g[2], plan, return_lse=True, scratch=False, **kw)
+    assert torch.equal(o1, o0) and torch.equal(l1, l0)
+    rows = [set(r) for r in om.build_frame_mask(T, P, 2, 1, 8, offset=3).rows]
+    for b in range(B):
+        ro, _ = oa.per_frame_sdpa(g[0][b:b + 1].float(), g[1][b:b + 1].float(), g[2][b:b + 1].float(), rows, P,
+                                  k_extra=g[4][b:b + 1].float() if n_txt else None,
+                                  v_extra=g[5][b:b + 1].float() if n_txt else None, frames=[0, T // 2, T - 1])
+        _close(o1[b:b + 1], ro, f"queued, batch {b}")
+    if n_txt:
+        _close(ot1, ot0.float(), "queued text vs unsplit", max_abs=8e-3, mean_abs=5e-4)
+        rto, _ = oa.text_row_attention(g[3][:1].float(), g[1][:1].float(), g[2][:1].float(), g[4][:1].float(),
+                                       g[5][:1].float())
+        _close(ot1[:1], rto, "queued text rows")
 
 
 def test_single_prefill_long_keys_split(gpu):
