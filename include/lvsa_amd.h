@@ -212,12 +212,19 @@ typedef struct lvsa_attn_args {
   const uint32_t* rel; int32_t words, R, C, q_frame0;
   int64_t q_tok0, k_tok0;
   int32_t rel_rows;
-  /* optional scratch (device memory, lvsa_attn_workspace_query bytes): with
-   * it, each text-query tile's key range is split into chunks that run as
-   * separate work-groups after the video tiles and are merged by a second
-   * launch (exact log-sum-exp merge, as flashinfer_runner.py:184-197), so the
-   * long text tiles fill the launch's last round instead of lengthening it.
-   * Null: text tiles run whole, first.                                        */
+  /* optional scratch (device memory, lvsa_attn_workspace_query bytes, 16-byte
+   * aligned; its contents on entry do not matter).  With it:
+   * - each text-query tile's key range is split into chunks that run as
+   *   separate work items after the video tiles and are merged by a second
+   *   launch (exact log-sum-exp merge, as flashinfer_runner.py:184-197), so
+   *   the long text tiles fill the launch's last round instead of
+   *   lengthening it;
+   * - the single-stream kernel (D = 64 and 128) runs one persistent
+   *   work-group per CU that takes work items from eight per-XCD queues
+   *   (counters in the last 1 KiB, zeroed by the call) and steals from the
+   *   other XCDs' queues once its own is empty, so XCDs that run faster take
+   *   over items of slower ones.
+   * Null: one work-group per work item, text tiles whole and first.          */
   void* workspace;
   int64_t workspace_bytes;
 } lvsa_attn_args;
@@ -228,8 +235,9 @@ typedef struct lvsa_attn_args {
  * encoder-query attention (lvsa/lvsa_processor.py:710-735) with one launch.   */
 LVSA_API int lvsa_attn_fwd(const lvsa_attn_args* a, hipStream_t stream);
 
-/* Bytes of scratch lvsa_attn_fwd uses for the text-tile split of `a`
- * (0 when there are no text queries); host only, nothing is launched.
+/* Bytes of scratch lvsa_attn_fwd uses for `a`: the text-tile split
+ * partials (none without text queries) and 1 KiB of work-queue counters;
+ * host only, nothing is launched.
  * Replaces the float workspace the FlashInfer wrapper is planned with
  * (flashinfer_runner.py:75-79, lvsa/lvsa_processor.py:798-804: 128 MB).      */
 LVSA_API int lvsa_attn_workspace_query(const lvsa_attn_args* a, int64_t* bytes);
@@ -237,9 +245,10 @@ LVSA_API int lvsa_attn_workspace_query(const lvsa_attn_args* a, int64_t* bytes);
 /* lvsa_attn_fwd without any allocation, for callers that cannot allocate
  * device memory (code under HIP graph capture, tight serving loops, harnesses
  * that forbid hipMalloc).  It has no counterpart in the reference.  The
- * scratch of the text-tile split comes from a static device array of
- * LVSA_NOALLOC_SCRATCH_BYTES per GPU (a->workspace is ignored), which each GPU
- * the library runs on holds until the process ends; a call that needs more
+ * scratch (work-queue counters and the text-tile split) comes from a static
+ * device array of LVSA_NOALLOC_SCRATCH_BYTES per GPU (a->workspace is
+ * ignored), which each GPU the library runs on holds until the process
+ * ends; a call that needs more
  * returns LVSA_ERR_CAPACITY.  All calls on one GPU share that array: calls
  * that overlap on one GPU (other streams, other threads) race, so serialise
  * them.  The caller still passes inputs and outputs; nothing else differs
