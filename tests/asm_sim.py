@@ -371,6 +371,15 @@ class Wave:
                 hi = (p >> 16).astype(np.uint16).view(np.float16).astype(np.float32)
             acc = self.vsrc_f(a[0])
             self.vdst(a[0], (acc + lo + hi).astype(np.float32))
+        elif op in ('v_dot2_f32_bf16', 'v_dot2_f32_f16'):
+            def pairs(x):
+                if op.endswith('bf16'):
+                    return bf16_to_f32(x & 0xFFFF), bf16_to_f32(x >> 16)
+                return ((x & 0xFFFF).astype(np.uint16).view(np.float16).astype(np.float32),
+                        (x >> 16).astype(np.uint16).view(np.float16).astype(np.float32))
+            a0, a1 = pairs(self.vsrc_u(a[1]))
+            b0, b1 = pairs(self.vsrc_u(a[2]))
+            self.vdst(a[0], (a0 * b0 + a1 * b1 + self.vsrc_f(a[3])).astype(np.float32))
         elif op == 'v_mov_b32':
             self.vdst(a[0], self.vsrc_u(a[1]))
         elif op == 'v_add_f32':
@@ -420,7 +429,8 @@ class Wave:
 
 class Sim:
     def __init__(self, dt='bf16', **opts):
-        lines = G.Gen(dt, **opts).build()
+        # the product's loop for the head size, with any options of the test on top
+        lines = G.Gen(dt, **{**G.PRODUCT[opts.get("D", 128)], **opts}).build()
         self.prog, self.labels = parse_program(lines)
         self.mem = Mem()
         self.lds = bytearray(131072)
