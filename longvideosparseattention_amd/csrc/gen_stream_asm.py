@@ -126,7 +126,8 @@ class Gen:
     def __init__(self, dt: str, D: int = 128, pad: bool = False, always_rare: bool = False, la: int = LA,
                  pv_b128: bool = False, no_softmax: bool = False, order: str = "group",
                  no_barrier: bool = False, no_decode: bool = False, no_exp: bool = False,
-                 lead: int = 0, early_load: bool = False, no_mask: bool = False, dot_init: bool = False):
+                 lead: int = 0, early_load: bool = False, no_mask: bool = False, dot_init: bool = False,
+                 and_scc: bool = False, copy_split: bool = False, sm_start: int = 2):
         assert dt in ("bf16", "f16")
         self.dt = dt
         self.L = Layout(D)
@@ -143,6 +144,9 @@ class Gen:
         self.early_load = early_load    # plan entry j+3 loaded in the middle of block j, not after it
         self.no_mask = no_mask          # timing only (wrong results): masks not applied
         self.dot_init = dot_init        # row-sum chains start with v_dot2 (C = 0) instead of two v_mov
+        self.and_scc = and_scc          # mask test branches on the SCC of s_and (no s_cmp)
+        self.copy_split = copy_split    # M0 of a copy set one MFMA slot ahead (no s_nop)
+        self.sm_start = sm_start        # first MFMA slot of a sub-iteration's softmax (mask test one before)
         self.lines: list[str] = []
         self.stubs: list[str] = []
 
@@ -214,8 +218,8 @@ class Gen:
             return []
         self.stubs += [f"{lbl('MSTUB_' + site)}:", f"s_mov_b32 s91, {sr(desc)}", f"s_mov_b32 s75, {32 * half}",
                        f"s_call_b64 {sr(S_RET, 2)}, {lbl('MASK_' + sset)}", f"s_branch {lbl('MRET_' + site)}"]
-        return [f"s_and_b32 s74, {sr(desc)}, 3", "s_cmp_lg_u32 s74, 0", f"s_cbranch_scc1 {lbl('MSTUB_' + site)}",
-                f"{lbl('MRET_' + site)}:"]
+        test = [f"s_and_b32 s74, {sr(desc)}, 3"] + ([] if self.and_scc else ["s_cmp_lg_u32 s74, 0"])
+        return test + [f"s_cbranch_scc1 {lbl('MSTUB_' + site)}", f"{lbl('MRET_' + site)}:"]
 
     def rare_routine(self, S: int, P: int, name: str) -> list[str]:
         """True row max of the sub-block, m -> max(m, max*cs), O and l rescaled, P recomputed."""
@@ -339,6 +343,17 @@ class Gen:
         return [f"s_add_u32 m0, {sr(S_LDSK)}, {lds}", "s_nop 0",
                 f"buffer_load_dwordx4 {vr(L.DV if v else L.DK)}, {sr(rs, 4)}, {so} offen lds"]
 
+    def place_copy(self, fill: dict[int, list[str]], at: int, stage: int, k: int) -> None:
+        """Copy k of a block after MFMA `at`; with copy_split, its M0 is set after
+        MFMA at - 1 (an MFMA and its operand reads in between cover the M0 ->
+        LDS-copy wait state)."""
+        c = self.copy(stage, k)
+        if self.copy_split and at > 0:
+            fill.setdefault(at - 1, []).append(c[0])
+            fill.setdefault(at, []).append(c[2])
+        else:
+            fill.setdefault(at, []).extend(c)
+
     # ── an MFMA stream with its operand reads and the interleaved work ──
     def stream(self, mfmas: list[tuple], fill: dict[int, list[str]], pre: int = 0,
                nxt: list[tuple] = ()) -> None:
@@ -439,16 +454,17 @@ class Gen:
         fill: dict[int, list[str]] = {0: [] if self.no_decode else self.decode(S_ENT + 2 * cst, site)}
         at_copy = (6, 10, 22, 26) if L.NCP == 2 else (5, 13)
         for k, at in enumerate(at_copy):
-            fill.setdefault(at, []).extend(self.copy(cst, k))
+            self.place_copy(fill, at, cst, k)
+        sm = self.sm_start
         # sub-iteration a: softmax of sub-block 2j-1 (S_B, block j-1 half 1)
-        fill.setdefault(1, []).extend(self.mask_check(site + "a", "B", S_ENT + 2 * vst + 1, 1))
-        self.spread(self.softmax_ops(L.SB, L.PB), list(range(2, M - 1)), fill)
+        fill.setdefault(sm - 1, []).extend(self.mask_check(site + "a", "B", S_ENT + 2 * vst + 1, 1))
+        self.spread(self.softmax_ops(L.SB, L.PB), list(range(sm, M - 1)), fill)
         fill.setdefault(M - 1, []).extend(self.softmax_tail(site + "a", "B"))
         # sub-iteration b: softmax of sub-block 2j (S_A, block j half 0)
-        fill.setdefault(M + 1, []).extend(self.mask_check(site + "b", "A", S_ENT + 2 * stage + 1, 0))
         if self.early_load:
             fill.setdefault(M, []).extend(self.entry_load(stage))
-        self.spread(self.softmax_ops(L.SA, L.PA), list(range(M + 2, 2 * M - 1)), fill)
+        fill.setdefault(M + sm - 1, []).extend(self.mask_check(site + "b", "A", S_ENT + 2 * stage + 1, 0))
+        self.spread(self.softmax_ops(L.SA, L.PA), list(range(M + sm, 2 * M - 1)), fill)
         fill.setdefault(2 * M - 1, []).extend(self.softmax_tail(site + "b", "A"))
         lead = self.lead_pv(vst)
         self.stream(mf, fill, pre=len(lead), nxt=self.lead_pv(stage))
@@ -461,7 +477,7 @@ class Gen:
         mf = [("qk", 0, 0, c, L.SA) for c in range(L.NQK)] + [("qk", 0, 1, c, L.SB) for c in range(L.NQK)]
         fill: dict[int, list[str]] = {0: self.decode(S_ENT + 4, "F")}
         for k in range(2 * L.NCP):
-            fill.setdefault(1 + k, []).extend(self.copy(2, k))
+            self.place_copy(fill, 1 + k, 2, k)
         fill.setdefault(L.NQK + 1, []).extend(self.mask_check("F", "A", S_ENT + 1, 0))
         self.spread(self.softmax_ops(L.SA, L.PA), list(range(L.NQK + 2, 2 * L.NQK - 1)), fill)
         fill.setdefault(2 * L.NQK - 1, []).extend(self.softmax_tail("F", "A"))
@@ -539,18 +555,22 @@ def operands(D: int) -> list[str]:
 # same loop without them): D = 128 opens each block with two PV MFMAs whose
 # operands were read before the barrier and loads plan entries mid-block
 # (0.4% faster on Wan 4x); both head sizes start the row-sum chains with a
-# non-accumulating v_dot2 (Wan 4x 0.8%, HunyuanVideo 1.1%, CogVideoX neutral).
-PRODUCT = {128: dict(lead=2, early_load=True, dot_init=True), 64: dict(dot_init=True)}
+# non-accumulating v_dot2 (Wan 4x 0.8%, HunyuanVideo 1.1%, CogVideoX neutral),
+# branch on the SCC of the mask test's s_and and set a copy's M0 one MFMA
+# slot early (together 0.6% on Wan 4x, CogVideoX neutral).  Measured neutral
+# and not used: the D = 64 softmax spread over one more MFMA slot (sm_start 1).
+PRODUCT = {128: dict(lead=2, early_load=True, dot_init=True, and_scc=True, copy_split=True),
+           64: dict(dot_init=True, and_scc=True, copy_split=True)}
 
 
-def render(**opts) -> str:
+def render(per_d: dict | None = None, **opts) -> str:
     out = ["// Generated by gen_stream_asm.py: the hand-scheduled key loops of",
            "// attn_fwd_stream_kernel (lvsa_attn_stream.h) and their asm operand lists.",
            "// Do not edit; regenerate.",
            "#pragma once", ""]
     for D in (128, 64):
         for dt, name in (("bf16", f"LVSA_STREAM{D}_LOOP_BF16"), ("f16", f"LVSA_STREAM{D}_LOOP_F16")):
-            lines = Gen(dt, D=D, **{**PRODUCT[D], **opts}).build()
+            lines = Gen(dt, D=D, **{**PRODUCT[D], **opts, **(per_d or {}).get(D, {})}).build()
             out.append(f"#define {name} \\")
             for ln in lines:
                 if not ln:
