@@ -168,9 +168,10 @@ LVSA_API int lvsa_plan_sizes_query(const lvsa_plan_params* p, int32_t max_row_fr
  *     word0 = (source << 31) | key-block index
  *     word1 = mask descriptor: bits 0-1 kind (0 none, 1 two-part, 2 generic),
  *             bits 2-5 allow bits (qa.lo, qa.hi, qb.lo, qb.hi),
- *             bits 8-15 key split within the block, bits 16-23 row split
+ *             bits 8-15 key split within the block, bits 16-24 row split
  *             (255 when the tile has a single query part).
- *   block_q <= 256, block_k <= 255; lvsa_attn_fwd runs tiles of 128 or 256
+ *   block_q <= 384, block_k <= 255; lvsa_attn_fwd runs tiles of 128, 256 or
+ *   (head size 64, 16-bit, frames of at least 383 query and 64 key rows) 384
  *   query rows (lvsa_attn_args.block_q) over key blocks of 64.               */
 LVSA_API int lvsa_plan_build(const lvsa_plan_params* p, int32_t* tile_indptr, uint32_t* entries,
                     int64_t max_entries, void* workspace, int64_t workspace_bytes,

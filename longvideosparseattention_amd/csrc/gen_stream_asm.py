@@ -75,11 +75,18 @@ LA = 3                            # MFMAs of LDS operand lookahead (< NSLOT); 3 
 
 
 class Layout:
-    """Head-size dependent shapes and the VGPR map."""
+    """Head-size dependent shapes and the VGPR map.  `nw` = 12 is the compact
+    map of the 12-wave kernel (three waves per SIMD, at most 168 VGPRs in all):
+    four operand slots read two MFMAs ahead, eight softmax temporaries, and the
+    rare path's temporaries shared with them."""
 
-    def __init__(self, D: int):
-        assert D in (64, 128)
+    def __init__(self, D: int, nw: int = 8, rs: bool = False):
+        assert D in (64, 128) and nw in (8, 12) and (nw == 8 or D == 64)
         self.D = D
+        self.nw = nw
+        self.rs = rs                      # row sums by MFMA: ONES (A pattern) and RS (result) tiles
+        self.nslot = NSLOT if nw == 8 else 4
+        self.NT = 16 if nw == 8 else 8       # softmax temporaries
         self.NQK = D // 16                # MFMA k-steps of a score tile
         self.NDT = D // 32                # 32-wide d-tiles of O
         self.RB = 2 * D                   # bytes per K/V row in LDS
@@ -96,18 +103,28 @@ class Layout:
         self.Q = take(4 * self.NQK)
         self.SA, self.SB = take(16), take(16)
         self.PA, self.PB = take(8), take(8)
-        self.OPS = take(4 * NSLOT)
+        self.OPS = take(4 * self.nslot)
         self.KOFF = take(self.NQK)
         self.VOFFA = take(self.NDT)
         self.VOFFB = take(self.NDT)
-        self.VM, self.VL, self.LS0, self.LS1 = take(1), take(1), take(1), take(1)
+        if rs:
+            self.VM, self.VL = take(1), take(1)
+            self.ONES, self.RS = take(4), take(4)
+            self.LS0 = self.LS1 = self.RS        # the row sum of the sub-block: RS register 0
+        else:
+            self.VM, self.VL, self.LS0, self.LS1 = take(1), take(1), take(1), take(1)
         self.DMAROW, self.C16, self.DK, self.DV = take(1), take(1), take(1), take(1)
         self.ROW, self.H4, self.NEGINF, self.VT = take(1), take(1), take(1), take(1)
-        self.RT = take(4)
-        self.T = take(16)
+        if nw == 8:
+            self.RT = take(4)
+            self.T = take(16)
+        else:
+            self.T = take(self.NT)
+            self.RT = self.T                 # the rare path runs between softmaxes
         self.NVGPR = r
-        self.CLOBBER_V = (list(range(self.SA, self.KOFF)) + [self.LS0, self.LS1, self.DK, self.DV] +
-                          list(range(self.RT, self.NVGPR)))
+        sums = list(range(self.RS, self.RS + 4)) if rs else [self.LS0, self.LS1]
+        self.CLOBBER_V = (list(range(self.SA, self.KOFF)) + sums + [self.DK, self.DV] +
+                          list(range(min(self.RT, self.T), self.NVGPR)))
 
 
 def vr(a: int, n: int = 1) -> str:
@@ -123,17 +140,20 @@ def lbl(name: str) -> str:
 
 
 class Gen:
-    def __init__(self, dt: str, D: int = 128, pad: bool = False, always_rare: bool = False, la: int = LA,
+    def __init__(self, dt: str, D: int = 128, nw: int = 8, pad: bool = False, always_rare: bool = False,
+                 la: int | None = None,
                  pv_b128: bool = False, no_softmax: bool = False, order: str = "group",
                  no_barrier: bool = False, no_decode: bool = False, no_exp: bool = False,
                  lead: int = 0, early_load: bool = False, no_mask: bool = False, dot_init: bool = False,
-                 and_scc: bool = False, copy_split: bool = False, sm_start: int = 2):
+                 and_scc: bool = False, copy_split: bool = False, sm_start: int = 2, rs_mfma: bool = False):
         assert dt in ("bf16", "f16")
         self.dt = dt
-        self.L = Layout(D)
+        self.L = Layout(D, nw, rs=rs_mfma)
+        self.rs_mfma = rs_mfma          # row sums by two 16x16x32 MFMAs against a ones pattern, no v_dot2
         self.pad = pad                  # diagnostics: 16 wait states after every MFMA
         self.always_rare = always_rare  # diagnostics: exact row max on every sub-block
-        self.la = la                    # MFMAs of LDS operand lookahead
+        self.la = (LA if nw == 8 else 2) if la is None else la   # MFMAs of LDS operand lookahead
+        assert self.la < self.L.nslot
         self.pv_b128 = pv_b128          # timing only (wrong results): one b128 read per PV operand
         self.no_softmax = no_softmax    # timing only (wrong results): no softmax VALU
         self.order = order              # softmax op order: "group" (4 fma, 4 exp) or "mix"
@@ -166,15 +186,36 @@ class Gen:
         cvt = "v_cvt_pk_bf16_f32" if self.dt == "bf16" else "v_cvt_pk_f16_f32"
         one = "0x3f803f80" if self.dt == "bf16" else "0x3c003c00"
         dot = "v_dot2c_f32_bf16" if self.dt == "bf16" else "v_dot2c_f32_f16"
-        fma = lambda k: f"v_fma_f32 {vr(L.T + k)}, {vr(S + k)}, {sr(S_CS)}, -{vr(L.VM)}"  # noqa: E731
-        exp = lambda k: ("s_nop 0" if self.no_exp else f"v_exp_f32 {vr(L.T + k)}, {vr(L.T + k)}")  # noqa: E731
-        pk = lambda q: f"{cvt} {vr(P + q)}, {vr(L.T + 2 * q)}, {vr(L.T + 2 * q + 1)}"  # noqa: E731
+        t = lambda k: L.T + k % L.NT  # noqa: E731   (eight temporaries: groups g and g + 2 share)
+        fma = lambda k: f"v_fma_f32 {vr(t(k))}, {vr(S + k)}, {sr(S_CS)}, -{vr(L.VM)}"  # noqa: E731
+        exp = lambda k: ("s_nop 0" if self.no_exp else f"v_exp_f32 {vr(t(k))}, {vr(t(k))}")  # noqa: E731
+        pk = lambda q: f"{cvt} {vr(P + q)}, {vr(t(2 * q))}, {vr(t(2 * q + 1))}"  # noqa: E731
         dot3 = "v_dot2_f32_bf16" if self.dt == "bf16" else "v_dot2_f32_f16"
 
         def d2(q: int) -> str:
             if self.dot_init and q < 2:   # first term of each chain: C = 0, the ones pair in S_ONE
                 return f"{dot3} {vr(L.LS0 + q)}, {sr(S_ONE)}, {vr(P + q)}, 0"
             return f"{dot} {vr(L.LS0 + (q & 1))}, {one}, {vr(P + q)}"
+        if self.rs_mfma:
+            # Row sums on the matrix core: P of 16 keys (the B operand layout of the
+            # 32x32x16 PV MFMA: lane l = query l%32, keys 8(l/32)..) read as the B
+            # operand of v_mfma_f32_16x16x32 is B[k][n] with n = l%16 and k-group
+            # l/16 = (key half, query >= 16); the ONES pattern (lanes 0, 32: row 0,
+            # k-groups 0, 2; lanes 20, 52: row 4, k-groups 1, 3) puts the full row
+            # sum of query l in register 0 of lanes 0-31 (lanes 32-63: zero).
+            mf16 = "v_mfma_f32_16x16x32_bf16" if self.dt == "bf16" else "v_mfma_f32_16x16x32_f16"
+            rs = lambda h: (f"{mf16} {vr(L.RS, 4)}, {vr(L.ONES, 4)}, {vr(P + 4 * h, 4)}, "  # noqa: E731
+                            f"{'0' if h == 0 else vr(L.RS, 4)}")
+            ops = []
+            for g in range(4):
+                ops += [fma(4 * g + i) for i in range(4)]
+                if g:
+                    ops += [pk(2 * g - 2), pk(2 * g - 1)]
+                ops += [exp(4 * g + i) for i in range(4)]
+                if g == 3:
+                    ops.append(rs(0))            # P + 0..3 packed in groups 1 and 2
+            ops += [pk(6), pk(7), "s_nop 1", rs(1)]   # VALU write -> MFMA read: 2 states
+            return ops
         ops = [] if self.dot_init else [f"v_mov_b32 {vr(L.LS0)}, 0", f"v_mov_b32 {vr(L.LS1)}, 0"]
         if self.order == "mix":
             # one exponential between two other ops: fma k+2, exp k; packs and dots
@@ -206,8 +247,12 @@ class Gen:
         L = self.L
         self.stubs += [f"{lbl('RSTUB_' + site)}:", f"s_call_b64 {sr(S_RET, 2)}, {lbl('RARE_' + sset)}",
                        f"s_branch {lbl('RRET_' + site)}"]
-        return ["s_nop 2",                                         # dot2 result -> VALU: 3 states
-                f"v_add_f32 {vr(L.LS0)}, {vr(L.LS0)}, {vr(L.LS1)}",
+        if self.rs_mfma:
+            head = ["s_nop 7", "s_nop 3"]                      # 16x16x32 MFMA result -> VALU
+        else:
+            head = ["s_nop 2",                                 # dot2 result -> VALU: 3 states
+                    f"v_add_f32 {vr(L.LS0)}, {vr(L.LS0)}, {vr(L.LS1)}"]
+        return head + [
                 f"v_cmp_nge_f32 vcc, 0x43800000, {vr(L.LS0)}",    # !(256 >= ls): ls > 256 or NaN
                 f"s_branch {lbl('RSTUB_' + site)}" if self.always_rare else f"s_cbranch_vccnz {lbl('RSTUB_' + site)}",
                 f"{lbl('RRET_' + site)}:",
@@ -248,7 +293,10 @@ class Gen:
              f"v_mul_f32 {vr(L.VL)}, {vr(RT + 1)}, {vr(L.VL)}"]
         r += [f"v_mul_f32 {vr(L.O + k)}, {vr(RT + 1)}, {vr(L.O + k)}" for k in range(16 * L.NDT)]
         r += self.softmax_ops(S, P)
-        r += ["s_nop 2", f"v_add_f32 {vr(L.LS0)}, {vr(L.LS0)}, {vr(L.LS1)}", f"s_setpc_b64 {sr(S_RET, 2)}"]
+        if self.rs_mfma:
+            r += ["s_nop 7", "s_nop 3", f"s_setpc_b64 {sr(S_RET, 2)}"]
+        else:
+            r += ["s_nop 2", f"v_add_f32 {vr(L.LS0)}, {vr(L.LS0)}, {vr(L.LS1)}", f"s_setpc_b64 {sr(S_RET, 2)}"]
         return r
 
     def mask_routine(self, S: int, name: str) -> list[str]:
@@ -260,7 +308,7 @@ class Gen:
         L = self.L
         r = [f"{lbl(name)}:",
              "s_bfe_u32 s88, s91, 0x80008",       # kb
-             "s_bfe_u32 s89, s91, 0x80010",       # qs
+             "s_bfe_u32 s89, s91, 0x90010",       # qs (9 bits: tiles of up to 384 rows)
              "s_bfe_u32 s90, s91, 0x40002",       # allow bits
              "s_sub_u32 s88, s88, s75",
              f"v_cmp_ge_u32_e64 s[78:79], {vr(L.ROW)}, s89",   # lanes of part b
@@ -359,7 +407,7 @@ class Gen:
                nxt: list[tuple] = ()) -> None:
         """mfmas: ("qk", stage, half, c, S) or ("pv", stage, st16, dt, P).
         fill[i]: instructions emitted right after MFMA i.  The LDS operands of MFMA i
-        go to slot i % NSLOT and are read LA MFMAs ahead.  The operands of the first
+        go to slot i % nslot and are read `la` MFMAs ahead.  The operands of the first
         `pre` MFMAs were read by the previous stream; `nxt` are the first MFMAs of the
         next stream, whose operands this one reads as if they followed it."""
         L = self.L
@@ -370,7 +418,7 @@ class Gen:
 
         def reads(i: int) -> list[str]:
             m = seq[i]
-            slot = L.OPS + 4 * (i % NSLOT)
+            slot = L.OPS + 4 * (i % L.nslot)
             if m[0] == "qk":
                 _, st, half, c, _ = m
                 return [f"ds_read_b128 {vr(slot, 4)}, {vr(L.KOFF + c)} offset:{st * L.TILE + half * 32 * L.RB}"]
@@ -388,7 +436,7 @@ class Gen:
             pending = sum(nreads[j] for j in range(max(i + 1, pre), issued))
             self.e(f"s_waitcnt lgkmcnt({min(15, pending)})")
             m = mfmas[i]
-            slot = L.OPS + 4 * (i % NSLOT)
+            slot = L.OPS + 4 * (i % L.nslot)
             if m[0] == "qk":
                 _, _, _, c, S = m
                 self.e(f"{self.mfma} {vr(S, 16)}, {vr(slot, 4)}, {vr(L.Q + 4 * c, 4)}, {'0' if c == 0 else vr(S, 16)}")
@@ -532,19 +580,26 @@ class Gen:
         return self.lines
 
 
-def operands(D: int) -> list[str]:
+def prefix(D: int, nw: int) -> str:
+    return f"LVSA_STREAM{D}" + ("" if nw == 8 else f"W{nw}")
+
+
+def operands(D: int, nw: int = 8, rs: bool = False) -> list[str]:
     """Macros with the asm operand lists of the D kernel (outputs, inputs, clobbers)."""
-    L = Layout(D)
+    L = Layout(D, nw, rs)
+    pf = prefix(D, nw)
     os_ = ", ".join(f"o{t}" for t in range(L.NDT))
     outs = ", ".join(f'"+{{{vr(L.O + 16 * t, 16)}}}"(o{t})' for t in range(L.NDT))
     outs += f', "+{{{vr(L.VM, 2)}}}"(ml), "+{{{vr(L.ROW, 4)}}}"(misc)'
     ins = (f'"{{{vr(L.Q, 4 * L.NQK)}}}"(qv), "{{{vr(L.KOFF, L.NQK)}}}"(koff), '
            f'"{{{vr(L.VOFFA, 2 * L.NDT)}}}"(voff), "{{{vr(L.DMAROW, 2)}}}"(dma), '
            f'"{{s[20:23]}}"(sa), "{{s[24:31]}}"(sb), "{{s[32:39]}}"(sc)')
+    if L.rs:
+        ins += f', "{{{vr(L.ONES, 4)}}}"(ones)'
     clob = [f'"v{r}"' for r in L.CLOBBER_V] + [f'"s{r}"' for r in CLOBBER_S]
-    out = [f"#define LVSA_STREAM{D}_OUTPUTS({os_}, ml, misc) {outs}",
-           f"#define LVSA_STREAM{D}_INPUTS(qv, koff, voff, dma, sa, sb, sc) {ins}",
-           f"#define LVSA_STREAM{D}_CLOBBERS \\"]
+    out = [f"#define {pf}_OUTPUTS({os_}, ml, misc) {outs}",
+           f"#define {pf}_INPUTS(qv, koff, voff, dma, sa, sb, sc, ones) {ins}",
+           f"#define {pf}_CLOBBERS \\"]
     for i in range(0, len(clob), 12):
         out.append("  " + ", ".join(clob[i:i + 12]) + ", \\")
     out.append('  "vcc", "m0", "scc", "memory"')
@@ -568,9 +623,11 @@ def render(per_d: dict | None = None, **opts) -> str:
            "// attn_fwd_stream_kernel (lvsa_attn_stream.h) and their asm operand lists.",
            "// Do not edit; regenerate.",
            "#pragma once", ""]
-    for D in (128, 64):
-        for dt, name in (("bf16", f"LVSA_STREAM{D}_LOOP_BF16"), ("f16", f"LVSA_STREAM{D}_LOOP_F16")):
-            lines = Gen(dt, D=D, **{**PRODUCT[D], **opts, **(per_d or {}).get(D, {})}).build()
+    for D, nw in ((128, 8), (64, 8), (64, 12)):
+        pf = prefix(D, nw)
+        for dt, name in (("bf16", f"{pf}_LOOP_BF16"), ("f16", f"{pf}_LOOP_F16")):
+            o = {**PRODUCT[D], **opts, **(per_d or {}).get(D, {})}
+            lines = Gen(dt, D=D, nw=nw, **o).build()
             out.append(f"#define {name} \\")
             for ln in lines:
                 if not ln:
@@ -580,7 +637,7 @@ def render(per_d: dict | None = None, **opts) -> str:
                 out.append(f'  "{ln}\\n" \\')
             out.append('  ""')
             out.append("")
-        out += operands(D)
+        out += operands(D, nw, o.get("rs_mfma", False))
         out.append("")
     return "\n".join(out)
 

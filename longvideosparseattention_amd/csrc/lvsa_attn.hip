@@ -156,8 +156,17 @@ extern "C" int lvsa_attn_fwd(const lvsa_attn_args* a, hipStream_t stream) {
   LVSA_REQUIRE(a->n_q >= 0 && a->n_k >= 0 && a->n_x >= 0 && a->n_tq >= 0, LVSA_ERR_INVALID_ARG,
                "lvsa_attn_fwd: negative length");
   LVSA_REQUIRE(a->tile_indptr && a->entries, LVSA_ERR_INVALID_ARG, "lvsa_attn_fwd: missing plan");
-  LVSA_REQUIRE(a->block_q == kBM || a->block_q == kPPBM, LVSA_ERR_UNSUPPORTED,
-               "lvsa_attn_fwd: block_q %d (the kernels tile 128 or 256 query rows)", a->block_q);
+  LVSA_REQUIRE(a->block_q == kBM || a->block_q == kPPBM || a->block_q == kStream12BM, LVSA_ERR_UNSUPPORTED,
+               "lvsa_attn_fwd: block_q %d (the kernels tile 128, 256 or 384 query rows)", a->block_q);
+  // 384-row tiles: the 12-wave single-stream kernel, head size 64 in 16 bit;
+  // its loop handles descriptors "none" and "two-part" only, which is all a
+  // plan holds when a tile touches at most two query frames (frames of at
+  // least 383 rows) and a key block at most two key frames (at least 64).
+  LVSA_REQUIRE(a->block_q != kStream12BM ||
+                   (a->D == 64 && !fp32 && (a->n_q == 0 || (a->R >= kStream12BM - 1 && a->C >= kBN))),
+               LVSA_ERR_UNSUPPORTED,
+               "lvsa_attn_fwd: 384-row tiles need head_dim 64 in bf16/fp16 and frames of >= 383 query and >= 64 "
+               "key rows (head_dim %d, R %d, C %d); build the plan with block_q 256", a->D, a->R, a->C);
   const int n_vt = (int)ceil_div(a->n_q, a->block_q), n_tt = (int)ceil_div(a->n_tq, a->block_q);
   LVSA_REQUIRE(a->n_video_tiles == n_vt && a->n_tiles == n_vt + n_tt, LVSA_ERR_INVALID_ARG,
                "lvsa_attn_fwd: plan has %d/%d tiles, expected %d/%d for block_q %d", a->n_video_tiles,
@@ -179,9 +188,10 @@ extern "C" int lvsa_attn_fwd(const lvsa_attn_args* a, hipStream_t stream) {
                LVSA_ERR_UNSUPPORTED, "lvsa_attn_fwd: key/value row stride too large");
   // the 256-row kernel forms per-lane row offsets with 24-bit multiplies
   auto fits24 = [&](int64_t row_elems) { return row_elems * 2 < (1LL << 24); };
-  LVSA_REQUIRE(a->block_q != kPPBM || (fits24(a->k_str[1]) && fits24(a->v_str[1]) &&
+  LVSA_REQUIRE(a->block_q == kBM || (fits24(a->k_str[1]) && fits24(a->v_str[1]) &&
                                        (a->n_x == 0 || (fits24(a->kx_str[1]) && fits24(a->vx_str[1])))),
-               LVSA_ERR_UNSUPPORTED, "lvsa_attn_fwd: key/value row stride of 16 MiB or more (block_q 256)");
+               LVSA_ERR_UNSUPPORTED, "lvsa_attn_fwd: key/value row stride of 16 MiB or more (block_q %d)",
+               a->block_q);
   // Every query row must have a relation row (generic blocks read it).
   if (a->n_q > 0) {
     const int64_t R = a->R > 0 ? a->R : 1;
@@ -265,6 +275,11 @@ extern "C" int lvsa_attn_fwd(const lvsa_attn_args* a, hipStream_t stream) {
                      (a->n_x == 0 || (fits32(a->n_x, a->kx_str[1]) && fits32(a->n_x, a->vx_str[1])));
   p.use_stream = (!fp32 && (a->D == 128 || a->D == 64) && a->block_q == kPPBM && !force_pp && src32 &&
                   (a->n_q == 0 || (p.R >= 255 && p.C >= 64))) ? 1 : 0;
+  if (a->block_q == kStream12BM) {
+    LVSA_REQUIRE(src32, LVSA_ERR_UNSUPPORTED,
+                 "lvsa_attn_fwd: 384-row tiles address each key source with 32-bit byte offsets (source too large)");
+    p.use_stream = 1;
+  }
   // With a workspace, the single-stream kernel runs one persistent
   // work-group per CU over the work queues (counters zeroed first).
   p.queues = nullptr;

@@ -8,10 +8,10 @@ namespace lvsa {
 int launch_d128(const AttnParams& prm, int block_q, bool bf16, hipStream_t stream) {
   if (block_q == kPPBM && prm.use_stream) {
     if (bf16) {
-      hipLaunchKernelGGL((attn_fwd_stream_kernel<128, __bf16>), dim3(prm.grid), dim3(kPPThreads), 0, stream,
+      hipLaunchKernelGGL((attn_fwd_stream_kernel<128, 8, __bf16>), dim3(prm.grid), dim3(kPPThreads), 0, stream,
                          prm);
     } else {
-      hipLaunchKernelGGL((attn_fwd_stream_kernel<128, _Float16>), dim3(prm.grid), dim3(kPPThreads), 0,
+      hipLaunchKernelGGL((attn_fwd_stream_kernel<128, 8, _Float16>), dim3(prm.grid), dim3(kPPThreads), 0,
                          stream, prm);
     }
     return launch_status("lvsa_attn_fwd");

@@ -812,6 +812,7 @@ __global__ __launch_bounds__(kThreads, D >= 192 ? 1 : 2) void attn_fwd_kernel(At
 constexpr int kPPWaves = 8;
 constexpr int kPPThreads = 64 * kPPWaves;
 constexpr int kPPBM = 32 * kPPWaves;
+constexpr int kStream12BM = 384;  // query rows per tile of the 12-wave single-stream kernel (D = 64)
 constexpr int kPPStages = 4;
 
 // Workgroup barrier that nothing crosses: the memory clobber orders LDS and

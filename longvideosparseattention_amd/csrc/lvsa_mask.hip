@@ -354,8 +354,8 @@ __device__ uint32_t frame_desc(const PlanCtx& c, int64_t r0, int qf0, int qf1, i
     const int64_t kb = two ? (kfb * p.C - p.k_tok0 - k0) : (k1 - k0);
     const uint32_t alo = rel_bit(c, qf0, kfa), ahi = two ? rel_bit(c, qf0, kfb) : 0u;
     const uint32_t blo = rel_bit(c, qf1, kfa), bhi = two ? rel_bit(c, qf1, kfb) : 0u;
-    // Row split inside the tile (1..block_q-1 <= 255).  Without a split both
-    // halves carry the same bits, so any value works; 255 is used.
+    // Row split inside the tile (1..block_q-1 <= 383: bits 16-24).  Without a
+    // split both halves carry the same bits, so any value works; 255 is used.
     const int64_t qs = (nq == 2) ? ((int64_t)(qf1 + p.q_frame0) * p.R - p.q_tok0 - r0) : 255;
     const bool all = alo && blo && (kb >= p.block_k || (ahi && bhi));
     if (all) return make_desc(kKindNone, 0, 0, 0);
@@ -585,8 +585,8 @@ static int plan_ctx(const lvsa_plan_params* p, PlanCtx* c) {
   LVSA_REQUIRE(p != nullptr, LVSA_ERR_INVALID_ARG, "lvsa_plan: null params");
   LVSA_REQUIRE(p->n_q >= 0 && p->n_k >= 0 && p->n_x >= 0 && p->n_tq >= 0, LVSA_ERR_INVALID_ARG,
                "lvsa_plan: negative length");
-  LVSA_REQUIRE(p->block_q >= 1 && p->block_q <= 256 && p->block_k >= 1 && p->block_k <= 255,
-               LVSA_ERR_INVALID_ARG, "lvsa_plan: block sizes (%d, %d) must lie in [1, 256] x [1, 255]",
+  LVSA_REQUIRE(p->block_q >= 1 && p->block_q <= 384 && p->block_k >= 1 && p->block_k <= 255,
+               LVSA_ERR_INVALID_ARG, "lvsa_plan: block sizes (%d, %d) must lie in [1, 384] x [1, 255]",
                p->block_q, p->block_k);
   LVSA_REQUIRE(p->n_q == 0 || (p->R >= 1 && p->C >= 1 && p->rel != nullptr && p->words >= 1 && p->rel_rows >= 1),
                LVSA_ERR_INVALID_ARG, "lvsa_plan: video rows need a relation (R, C, rel, words, rel_rows)");

@@ -29,14 +29,18 @@ def kernel_head_dim(head_dim: int) -> int:
     return head_dim
 
 
-def attn_block_q(head_dim: int = 128, dtype: Optional[torch.dtype] = None) -> int:
+def attn_block_q(head_dim: int = 128, dtype: Optional[torch.dtype] = None, frame_rows: int = 0,
+                 key_rows: int = 0) -> int:
     """Query rows per attention tile, i.e. which kernel a plan is built for.
 
-    256 for head sizes 64, 96 and 128: the 8-wave kernels (bf16 / fp16).
-    128 for 192 and 256: the 4-wave kernel (the 8-wave kernels' registers
-    hold no Q and O that wide), and for fp32 inputs at every head size (the
-    fp32 kernel).  ``LVSA_ATTN_BLOCK_Q`` (128 or 256) overrides the choice for
-    64 and 128 in 16-bit; 96 runs on the 8-wave kernel only."""
+    384 for head size 64 in 16-bit when query frames span at least 383 rows
+    and key frames at least 64 (``frame_rows``, ``key_rows``): the 12-wave
+    single-stream kernel, three waves per SIMD.  256 for head sizes 64, 96
+    and 128 otherwise: the 8-wave kernels (bf16 / fp16).  128 for 192 and 256:
+    the 4-wave kernel (the 8-wave kernels' registers hold no Q and O that
+    wide), and for fp32 inputs at every head size (the fp32 kernel).
+    ``LVSA_ATTN_BLOCK_Q`` (128, 256 or 384) overrides the choice for 64 and 128
+    in 16-bit (384: head size 64 only); 96 runs on the 8-wave kernel only."""
     kd = kernel_head_dim(head_dim)
     if dtype == torch.float32:
         return 128
@@ -47,6 +51,8 @@ def attn_block_q(head_dim: int = 128, dtype: Optional[torch.dtype] = None) -> in
     env = os.environ.get("LVSA_ATTN_BLOCK_Q")
     if env:
         return int(env)
+    if kd == 64 and frame_rows >= 383 and key_rows >= capi.ATTN_BLOCK_K:
+        return 384
     return 256
 
 

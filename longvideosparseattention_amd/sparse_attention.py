@@ -440,7 +440,7 @@ class LVSAMetadata:
         """Plan for ``lvsa_sdpa`` semantics: every query row attends all extra
         rows (``k_global``) plus the non-global window frames of its frame."""
         st = self.device_state(device)
-        block_q = hip_ops.attn_block_q(head_dim, dtype)
+        block_q = hip_ops.attn_block_q(head_dim, dtype, self.num_patches, self.num_patches)
         key = ("window", n_q, n_k, n_extra, block_q)
         plan = st.plans.get(key)
         if plan is None:
@@ -458,7 +458,7 @@ class LVSAMetadata:
         if self.world != 1:
             raise NotImplementedError("zero-copy LVSA attention needs the whole sequence on one GPU (world=1)")
         st = self.device_state(device)
-        block_q = hip_ops.attn_block_q(head_dim, dtype)
+        block_q = hip_ops.attn_block_q(head_dim, dtype, self.num_patches, self.num_patches)
         key = ("full", n_q, n_k, n_text_k, n_text_q, block_q)
         plan = st.plans.get(key)
         if plan is None:

@@ -431,6 +431,7 @@ class Sim:
     def __init__(self, dt='bf16', **opts):
         # the product's loop for the head size, with any options of the test on top
         lines = G.Gen(dt, **{**G.PRODUCT[opts.get("D", 128)], **opts}).build()
+        self.nw = opts.get("nw", 8)
         self.prog, self.labels = parse_program(lines)
         self.mem = Mem()
         self.lds = bytearray(131072)

@@ -104,7 +104,10 @@ def test_plan_sizes():
     assert lib.lvsa_plan_sizes_query(C.byref(p), 17, C.byref(s)) == 0
     assert s.n_tiles == s.n_video_tiles == 1024
     assert 0 < s.max_entries <= 1024 * 2048
-    p.block_q = 300
+    p.block_q = 384                          # the 12-wave kernel's tiles (row split in 9 bits)
+    assert lib.lvsa_plan_sizes_query(C.byref(p), 17, C.byref(s)) == 0
+    assert s.n_video_tiles == -(-131040 // 384)
+    p.block_q = 385
     assert lib.lvsa_plan_sizes_query(C.byref(p), 17, C.byref(s)) == -1
 
 
@@ -120,6 +123,15 @@ def test_attn_rejects_bad_args_without_launching():
     a.D, a.block_q = 192, 256
     assert lib.lvsa_attn_fwd(C.byref(a), None) == -2
     assert b"head_dim 192 runs 128-row tiles" in lib.lvsa_last_error()
+    a.tile_indptr = a.entries = 4096         # host checks only: nothing is launched
+    a.D, a.block_q = 128, 384                # 384-row tiles: head size 64 only
+    assert lib.lvsa_attn_fwd(C.byref(a), None) == -2
+    assert b"384-row tiles need head_dim 64" in lib.lvsa_last_error()
+    a.D, a.n_q, a.R, a.C = 64, 1000, 300, 300   # query frames below 383 rows
+    assert lib.lvsa_attn_fwd(C.byref(a), None) == -2
+    assert b"384-row tiles" in lib.lvsa_last_error()
+    a.n_q, a.R, a.C, a.block_q = 0, 0, 0, 256
+    a.tile_indptr = a.entries = None
     a.D, a.H, a.Hkv = 128, 3, 2
     assert lib.lvsa_attn_fwd(C.byref(a), None) == -1
 

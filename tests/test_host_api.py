@@ -150,6 +150,13 @@ def test_head_sizes_of_the_plugin():
     assert [hip_ops.kernel_head_dim(d) for d in (64, 96, 128, 192, 256)] == [64, 96, 128, 192, 256]
     assert hip_ops.attn_block_q(256) == 128 and hip_ops.attn_block_q(192) == 128
     assert hip_ops.attn_block_q(96) == 256
+    # head size 64: 384-row tiles (12 waves) when frames span >= 383 query and >= 64 key rows
+    assert hip_ops.attn_block_q(64, torch.bfloat16, 1350, 1350) == 384
+    assert hip_ops.attn_block_q(64, torch.float16, 383, 64) == 384
+    assert hip_ops.attn_block_q(64, torch.bfloat16, 382, 1350) == 256
+    assert hip_ops.attn_block_q(64, torch.bfloat16, 1350, 63) == 256
+    assert hip_ops.attn_block_q(64, torch.float32, 1350, 1350) == 128
+    assert hip_ops.attn_block_q(128, torch.bfloat16, 1560, 1560) == 256
     with pytest.raises(ValueError, match="head_dim 80"):
         hip_ops.kernel_head_dim(80)
 

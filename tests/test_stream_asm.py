@@ -39,26 +39,27 @@ def _allowed(y, row, key_in_block):
     """Reference meaning of a plan descriptor (lvsa_amd.h)."""
     if y & 3 == 0:
         return True
-    bits, kb, qs = (y >> 2) & 0xF, (y >> 8) & 0xFF, (y >> 16) & 0xFF
+    bits, kb, qs = (y >> 2) & 0xF, (y >> 8) & 0xFF, (y >> 16) & 0x1FF
     part_b = row >= qs
     lo = key_in_block < kb
     bit = (2 if part_b else 0) + (0 if lo else 1)
     return bool((bits >> bit) & 1)
 
 
-def run_loop(entries, nk, n_x, seed=0, dt="bf16", D=128, **opts):
-    """Run the generated loop for the 8 waves of one work-group with the
-    registers the C++ prologue of attn_fwd_stream_kernel sets up."""
+def run_loop(entries, nk, n_x, seed=0, dt="bf16", D=128, nw=8, **opts):
+    """Run the generated loop for the `nw` waves of one work-group with the
+    registers the C++ prologue of attn_fwd_stream_kernel sets up (the 12-wave
+    kernel: 384 query rows, waves 8-11 repeat the copies of waves 0-3)."""
     rng = np.random.default_rng(seed)
-    R = 256
-    L = A.G.Layout(D)
+    R = 32 * nw
+    L = A.G.Layout(D, nw)
     RB, NCH = 2 * D, D // 8
     rnd = (lambda x: A.bf16_to_f32(A.bf16_round(x))) if dt == "bf16" else (lambda x: x.astype(np.float16).astype(np.float32))
     enc = (lambda x: A.bf16_round(x).astype(np.uint16).tobytes()) if dt == "bf16" else (lambda x: x.astype(np.float16).tobytes())
     q = rnd(rng.standard_normal((R, D)).astype(np.float32))
     k, v = (rnd(rng.standard_normal((nk, D)).astype(np.float32)) for _ in range(2))
     kx, vx = (rnd(rng.standard_normal((max(n_x, 1), D)).astype(np.float32)) for _ in range(2))
-    sim = A.Sim(dt, D=D, **opts)
+    sim = A.Sim(dt, D=D, nw=nw, **opts)
     kb0, vb0, kb1, vb1 = (sim.mem.alloc(enc(x)) for x in (k, v, kx, vx))
     ep = sim.mem.alloc(b"".join(struct.pack("<II", x, y) for x, y in entries))
     scale = 1 / math.sqrt(D)
@@ -66,7 +67,7 @@ def run_loop(entries, nk, n_x, seed=0, dt="bf16", D=128, **opts):
     h, i32 = lane >> 5, lane & 31
     qbits = (A.bf16_round(q) if dt == "bf16" else q.astype(np.float16).view(np.uint16).astype(np.uint32))
     waves = []
-    for w in range(8):
+    for w in range(nw):
         W = A.Wave(w, sim)
         V = W.v
         rows = 32 * w + i32
@@ -85,7 +86,7 @@ def run_loop(entries, nk, n_x, seed=0, dt="bf16", D=128, **opts):
             V[L.VOFFA + dt_] = L.VBASE + rowA * RB + ((chunk ^ np.array([_swz(x, D) for x in rowA])) << 4) + inb
             V[L.VOFFB + dt_] = (L.VBASE + (rowA + 8) * RB +
                                 ((chunk ^ np.array([_swz(x, D) for x in rowA + 8])) << 4) + inb)
-        crow = w * (1024 // RB) + lane // NCH
+        crow = (w % 8) * (1024 // RB) + lane // NCH
         V[L.DMAROW] = crow
         V[L.C16] = ((lane % NCH) ^ np.array([_swz(x & 15, D) for x in crow])) * 16
         V[L.ROW], V[L.H4], V[L.NEGINF], V[L.VT] = 32 * w + i32, 4 * h, 0xFF800000, 0
@@ -96,7 +97,7 @@ def run_loop(entries, nk, n_x, seed=0, dt="bf16", D=128, **opts):
         for i, b in enumerate((kb0, vb0, kb1, vb1)):
             S[24 + 2 * i], S[25 + 2 * i] = b & 0xFFFFFFFF, b >> 32
         S[32:36] = [RB, RB, RB, RB]
-        S[36], S[37], S[38], S[39] = nk, n_x, w, 1024 * w
+        S[36], S[37], S[38], S[39] = nk, n_x, w, 1024 * (w % 8)
         waves.append(W)
     sim.run(waves)
     O = np.zeros((R, D))
@@ -153,6 +154,29 @@ def test_loop_matches_attention(case, D):
     assert err <= 4e-3 and lse_err <= 2e-3, (case, err, lse_err)
     # D/32 copies per wave per block for blocks 0..n+1 (the last two repeat block n-1)
     assert copies == 8 * (D // 32) * (len(entries) + 2)
+
+
+@pytest.mark.parametrize("case", sorted(CASES))
+def test_loop_12_waves(case):
+    """The 12-wave D = 64 loop (384 query rows, compact register map, waves
+    8-11 repeating the copies of waves 0-3)."""
+    make, nk, n_x = CASES[case]
+    err, lse_err, copies = run_loop(make(), nk, n_x, D=64, nw=12)
+    assert err <= 4e-3 and lse_err <= 2e-3, (case, err, lse_err)
+    assert copies == 12 * 2 * (len(make()) + 2)
+
+
+def test_loop_12_waves_row_split_past_255_and_rare_path():
+    """Row splits above row 255 (the 9-bit split of 384-row tiles) and the
+    exact-max path on every sub-block, 12 waves."""
+    entries = [(0, 0), (1, _desc_two_part(0b1011, 40, 300)), (2, _desc_two_part(0b0110, 64, 257)),
+               (3, _desc_two_part(0b1101, 17, 383))]
+    err, lse_err, _ = run_loop(entries, 256, 0, seed=5, D=64, nw=12)
+    assert err <= 4e-3 and lse_err <= 2e-3, (err, lse_err)
+    err, lse_err, _ = run_loop([(j, 0) for j in range(3)], 192, 0, seed=6, D=64, nw=12, always_rare=True)
+    assert err <= 4e-3 and lse_err <= 2e-3, (err, lse_err)
+    err, lse_err, _ = run_loop([(j, _tail(150, j)) for j in range(3)], 150, 0, seed=7, dt="f16", D=64, nw=12)
+    assert err <= 2e-3 and lse_err <= 2e-3, (err, lse_err)
 
 
 @pytest.mark.parametrize("D", [128, 64])
