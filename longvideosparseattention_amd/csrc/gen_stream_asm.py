@@ -24,7 +24,10 @@ has been in LDS since the previous barrier), so the matrix core has work
 while the first K operands of the block are read; `early_load` issues the
 scalar load of entry j + 3 in the middle of block j, not just before the
 barrier that waits for it; `dot_init` starts the two row-sum chains of a
-sub-block with a non-accumulating v_dot2 (C = 0) instead of zeroing them.
+sub-block with a non-accumulating v_dot2 (C = 0) instead of zeroing them;
+`rs_mfma` replaces those chains by two v_mfma_f32_16x16x32 per sub-block with
+A = a constant ones pattern and B = the packed P, which leave the full row sum
+of query l in lane l (l < 32) and zero in lanes 32-63.
 
 Softmax without a row max: P is formed against the running max m of the
 earlier blocks; m has to move only if some P exceeds 2^8, and then the
@@ -214,7 +217,7 @@ class Gen:
                 ops += [exp(4 * g + i) for i in range(4)]
                 if g == 3:
                     ops.append(rs(0))            # P + 0..3 packed in groups 1 and 2
-            ops += [pk(6), pk(7), "s_nop 1", rs(1)]   # VALU write -> MFMA read: 2 states
+            ops += [pk(6), pk(7), "s_nop 4", rs(1)]   # VALU write -> MFMA read of the packs
             return ops
         ops = [] if self.dot_init else [f"v_mov_b32 {vr(L.LS0)}, 0", f"v_mov_b32 {vr(L.LS1)}, 0"]
         if self.order == "mix":
@@ -612,10 +615,12 @@ def operands(D: int, nw: int = 8, rs: bool = False) -> list[str]:
 # (0.4% faster on Wan 4x); both head sizes start the row-sum chains with a
 # non-accumulating v_dot2 (Wan 4x 0.8%, HunyuanVideo 1.1%, CogVideoX neutral),
 # branch on the SCC of the mask test's s_and and set a copy's M0 one MFMA
-# slot early (together 0.6% on Wan 4x, CogVideoX neutral).  Measured neutral
+# slot early (together 0.6% on Wan 4x, CogVideoX neutral); both take the row
+# sums from two 16x16x32 MFMAs against a ones pattern instead of eight v_dot2
+# and an add per sub-block (Wan 4x 2.7%, CogVideoX 1.9%).  Measured neutral
 # and not used: the D = 64 softmax spread over one more MFMA slot (sm_start 1).
-PRODUCT = {128: dict(lead=2, early_load=True, dot_init=True, and_scc=True, copy_split=True),
-           64: dict(dot_init=True, and_scc=True, copy_split=True)}
+PRODUCT = {128: dict(lead=2, early_load=True, dot_init=True, and_scc=True, copy_split=True, rs_mfma=True),
+           64: dict(dot_init=True, and_scc=True, copy_split=True, rs_mfma=True)}
 
 
 def render(per_d: dict | None = None, **opts) -> str:

@@ -318,6 +318,37 @@ class Wave:
                         res[ln, j] = int(lds[x]) | (int(lds[x + 1]) << 8)
                 self.v[dreg, :] = res[:, 0] | (res[:, 1] << 16)
                 self.v[dreg + 1, :] = res[:, 2] | (res[:, 3] << 16)
+        elif op.startswith('v_mfma_f32_16x16x32'):
+            # lane l: A[l%16][8(l/16)..+7], B[8(l/16)..+7][l%16]; D register r of
+            # lane l is element (4(l/16) + r, l%16)
+            bf = op.endswith('bf16')
+            d, _ = self.vreg(a[0])
+            ra, _ = self.vreg(a[1])
+            rb, _ = self.vreg(a[2])
+            cv = None if a[3] == '0' else self.vreg(a[3])[0]
+            conv = (lambda h: bf16_to_f32(h)) if bf else (lambda h: (h & 0xFFFF).astype(np.uint16).view(np.float16).astype(np.float32))
+
+            def elems16(r0):
+                x = self.v[r0:r0 + 4].T
+                return np.stack([conv(x & 0xFFFF), conv(x >> 16)], axis=2).reshape(64, 8)
+            Ae, Be = elems16(ra), elems16(rb)
+            A = np.zeros((16, 32), dtype=np.float64)
+            B = np.zeros((32, 16), dtype=np.float64)
+            for ln in range(64):
+                A[ln % 16, 8 * (ln // 16):8 * (ln // 16) + 8] = Ae[ln]
+                B[8 * (ln // 16):8 * (ln // 16) + 8, ln % 16] = Be[ln]
+            Cm = np.zeros((16, 16), dtype=np.float64)
+            if cv is not None:
+                for ln in range(64):
+                    for r in range(4):
+                        Cm[4 * (ln // 16) + r, ln % 16] = u2f(self.v[cv + r, ln])
+            with np.errstate(invalid="ignore", over="ignore"):   # inf * 0 of the first block -> NaN
+                Dm = (A @ B + Cm).astype(np.float32)
+            out = np.zeros((4, 64), dtype=np.float32)
+            for ln in range(64):
+                for r in range(4):
+                    out[r, ln] = Dm[4 * (ln // 16) + r, ln % 16]
+            self.v[d:d + 4] = out.view(np.uint32)
         elif op.startswith('v_mfma_f32_32x32x16'):
             bf = op.endswith('bf16')
             d, _ = self.vreg(a[0])

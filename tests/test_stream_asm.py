@@ -52,7 +52,7 @@ def run_loop(entries, nk, n_x, seed=0, dt="bf16", D=128, nw=8, **opts):
     kernel: 384 query rows, waves 8-11 repeat the copies of waves 0-3)."""
     rng = np.random.default_rng(seed)
     R = 32 * nw
-    L = A.G.Layout(D, nw)
+    L = A.G.Layout(D, nw, rs=opts.get("rs_mfma", A.G.PRODUCT[D].get("rs_mfma", False)))
     RB, NCH = 2 * D, D // 8
     rnd = (lambda x: A.bf16_to_f32(A.bf16_round(x))) if dt == "bf16" else (lambda x: x.astype(np.float16).astype(np.float32))
     enc = (lambda x: A.bf16_round(x).astype(np.uint16).tobytes()) if dt == "bf16" else (lambda x: x.astype(np.float16).tobytes())
@@ -91,6 +91,10 @@ def run_loop(entries, nk, n_x, seed=0, dt="bf16", D=128, nw=8, **opts):
         V[L.C16] = ((lane % NCH) ^ np.array([_swz(x & 15, D) for x in crow])) * 16
         V[L.ROW], V[L.H4], V[L.NEGINF], V[L.VT] = 32 * w + i32, 4 * h, 0xFF800000, 0
         V[L.VM] = A.f2u(np.full(64, -1e30, np.float32))
+        if L.rs:
+            one = 0x3F803F80 if dt == "bf16" else 0x3C003C00
+            for j in range(4):
+                V[L.ONES + j] = np.where(np.isin(lane, [0, 20, 32, 52]), one, 0)
         S = W.s
         S[20], S[21], S[22] = ep & 0xFFFFFFFF, ep >> 32, len(entries)
         S[23] = int(A.f2u(np.float32(scale * 1.4426950408889634)))
