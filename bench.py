@@ -59,7 +59,9 @@ def parse(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=24)
-    ap.add_argument("--warmup", type=int, default=4)
+    # warm-up calls are untimed; 16 let the clock settle (a 2 ms CogVideoX call
+    # still ramps over its first ten or so)
+    ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--config", default="wan4x", choices=sorted(CONFIGS))
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-baseline sample budget")
     ap.add_argument("--no-cpu-baseline", action="store_true")
