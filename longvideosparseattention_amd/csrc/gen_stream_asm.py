@@ -52,7 +52,10 @@ Register map (VGPRs; the kernel's operands pin them), D = 128 (D = 64):
   operand slots (4 each), the K read offsets (one per k-step), the V^T read
   offsets (two per d-tile), then m, l, two partial row sums, the copy row and
   chunk, the two copy offsets, the tile row, 4*h, -inf, a mask temp, four
-  RARE temps and sixteen softmax temps: 224 (168) VGPRs in all.
+  RARE temps and sixteen softmax temps: 224 (168) VGPRs in all.  With
+  rs_mfma the two partial row sums give way to a ones pattern and a row-sum
+  tile (4 each).  The 12-wave D = 64 map (Layout nw = 12) has four operand
+  slots, eight softmax temps and the RARE temps inside them: 148 VGPRs.
 SGPRs: s[20:21] entry pointer, s22 blocks, s23 scale*log2(e), s[24:31] K/V
 bases (video, extra), s32-35 row strides, s36-37 source lengths, s38 wave,
 s39 LDS copy base of the wave; s40-s95 scratch.
@@ -148,11 +151,15 @@ class Gen:
                  pv_b128: bool = False, no_softmax: bool = False, order: str = "group",
                  no_barrier: bool = False, no_decode: bool = False, no_exp: bool = False,
                  lead: int = 0, early_load: bool = False, no_mask: bool = False, dot_init: bool = False,
-                 and_scc: bool = False, copy_split: bool = False, sm_start: int = 2, rs_mfma: bool = False):
+                 and_scc: bool = False, copy_split: bool = False, sm_start: int = 2, rs_mfma: bool = False,
+                 wait_pair: bool = False, rs_mix: bool = False, tail_nop: int = 12):
         assert dt in ("bf16", "f16")
         self.dt = dt
         self.L = Layout(D, nw, rs=rs_mfma)
         self.rs_mfma = rs_mfma          # row sums by two 16x16x32 MFMAs against a ones pattern, no v_dot2
+        self.wait_pair = wait_pair      # one LDS wait per two MFMAs (before the even one, for both)
+        self.rs_mix = rs_mix            # rs_mfma softmax with the exponentials interleaved one by one
+        self.tail_nop = tail_nop        # wait states between the last row-sum MFMA and its VALU read
         self.pad = pad                  # diagnostics: 16 wait states after every MFMA
         self.always_rare = always_rare  # diagnostics: exact row max on every sub-block
         self.la = (LA if nw == 8 else 2) if la is None else la   # MFMAs of LDS operand lookahead
@@ -210,6 +217,19 @@ class Gen:
             rs = lambda h: (f"{mf16} {vr(L.RS, 4)}, {vr(L.ONES, 4)}, {vr(P + 4 * h, 4)}, "  # noqa: E731
                             f"{'0' if h == 0 else vr(L.RS, 4)}")
             ops = []
+            if self.rs_mix:
+                # fma k+2, exp k; the pack of pair q two instructions after exp 2q+1
+                ops = [fma(0), fma(1)]
+                for k in range(16):
+                    if k + 2 < 16:
+                        ops.append(fma(k + 2))
+                    ops.append(exp(k))
+                    if k % 2 == 0 and k >= 2:
+                        ops.append(pk(k // 2 - 1))
+                    if k == 11:
+                        ops.append(rs(0))        # P + 0..3: packed by k = 8
+                ops += [pk(7), "s_nop 4", rs(1)]
+                return ops
             for g in range(4):
                 ops += [fma(4 * g + i) for i in range(4)]
                 if g:
@@ -250,8 +270,8 @@ class Gen:
         L = self.L
         self.stubs += [f"{lbl('RSTUB_' + site)}:", f"s_call_b64 {sr(S_RET, 2)}, {lbl('RARE_' + sset)}",
                        f"s_branch {lbl('RRET_' + site)}"]
-        if self.rs_mfma:
-            head = ["s_nop 7", "s_nop 3"]                      # 16x16x32 MFMA result -> VALU
+        if self.rs_mfma:                                       # 16x16x32 MFMA result -> VALU
+            head = ["s_nop 7"] + ([f"s_nop {self.tail_nop - 9}"] if self.tail_nop > 8 else [])
         else:
             head = ["s_nop 2",                                 # dot2 result -> VALU: 3 states
                     f"v_add_f32 {vr(L.LS0)}, {vr(L.LS0)}, {vr(L.LS1)}"]
@@ -436,8 +456,14 @@ class Gen:
         for i in range(pre, issued):
             self.e(*reads(i))
         for i in range(n):
-            pending = sum(nreads[j] for j in range(max(i + 1, pre), issued))
-            self.e(f"s_waitcnt lgkmcnt({min(15, pending)})")
+            if not self.wait_pair:
+                pending = sum(nreads[j] for j in range(max(i + 1, pre), issued))
+                self.e(f"s_waitcnt lgkmcnt({min(15, pending)})")
+            elif i >= pre and (i - pre) % 2 == 0:
+                # one wait for the operands of MFMAs i and i + 1 (the pre-read ones need none)
+                last = i + 1 if i + 1 < n else i
+                pending = sum(nreads[j] for j in range(last + 1, issued))
+                self.e(f"s_waitcnt lgkmcnt({min(15, pending)})")
             m = mfmas[i]
             slot = L.OPS + 4 * (i % L.nslot)
             if m[0] == "qk":
