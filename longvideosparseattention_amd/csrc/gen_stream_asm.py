@@ -152,7 +152,8 @@ class Gen:
                  no_barrier: bool = False, no_decode: bool = False, no_exp: bool = False,
                  lead: int = 0, early_load: bool = False, no_mask: bool = False, dot_init: bool = False,
                  and_scc: bool = False, copy_split: bool = False, sm_start: int = 2, rs_mfma: bool = False,
-                 wait_pair: bool = False, rs_mix: bool = False, tail_nop: int = 12):
+                 wait_pair: bool = False, rs_mix: bool = False, tail_nop: int = 12, no_switch: bool = False,
+                 no_fma: bool = False, qk_dup: bool = False, no_rare: bool = False, tail_split: bool = False):
         assert dt in ("bf16", "f16")
         self.dt = dt
         self.L = Layout(D, nw, rs=rs_mfma)
@@ -160,6 +161,11 @@ class Gen:
         self.wait_pair = wait_pair      # one LDS wait per two MFMAs (before the even one, for both)
         self.rs_mix = rs_mix            # rs_mfma softmax with the exponentials interleaved one by one
         self.tail_nop = tail_nop        # wait states between the last row-sum MFMA and its VALU read
+        self.no_switch = no_switch      # timing only (wrong with extra key rows): no key-source check
+        self.no_fma = no_fma            # timing only (wrong results): exp of S without scale and max
+        self.qk_dup = qk_dup            # timing only (wrong results): every QK MFMA issued twice
+        self.no_rare = no_rare          # timing only (wrong results): the rare-path branch never taken
+        self.tail_split = tail_split    # rare test issued one MFMA before its branch
         self.pad = pad                  # diagnostics: 16 wait states after every MFMA
         self.always_rare = always_rare  # diagnostics: exact row max on every sub-block
         self.la = (LA if nw == 8 else 2) if la is None else la   # MFMAs of LDS operand lookahead
@@ -199,6 +205,9 @@ class Gen:
         t = lambda k: L.T + k % L.NT  # noqa: E731   (eight temporaries: groups g and g + 2 share)
         fma = lambda k: f"v_fma_f32 {vr(t(k))}, {vr(S + k)}, {sr(S_CS)}, -{vr(L.VM)}"  # noqa: E731
         exp = lambda k: ("s_nop 0" if self.no_exp else f"v_exp_f32 {vr(t(k))}, {vr(t(k))}")  # noqa: E731
+        if self.no_fma:
+            fma = lambda k: None  # noqa: E731
+            exp = lambda k: f"v_exp_f32 {vr(t(k))}, {vr(S + k)}"  # noqa: E731
         pk = lambda q: f"{cvt} {vr(P + q)}, {vr(t(2 * q))}, {vr(t(2 * q + 1))}"  # noqa: E731
         dot3 = "v_dot2_f32_bf16" if self.dt == "bf16" else "v_dot2_f32_f16"
 
@@ -229,7 +238,7 @@ class Gen:
                     if k == 11:
                         ops.append(rs(0))        # P + 0..3: packed by k = 8
                 ops += [pk(7), "s_nop 4", rs(1)]
-                return ops
+                return [o for o in ops if o is not None]
             for g in range(4):
                 ops += [fma(4 * g + i) for i in range(4)]
                 if g:
@@ -238,7 +247,7 @@ class Gen:
                 if g == 3:
                     ops.append(rs(0))            # P + 0..3 packed in groups 1 and 2
             ops += [pk(6), pk(7), "s_nop 4", rs(1)]   # VALU write -> MFMA read of the packs
-            return ops
+            return [o for o in ops if o is not None]
         ops = [] if self.dot_init else [f"v_mov_b32 {vr(L.LS0)}, 0", f"v_mov_b32 {vr(L.LS1)}, 0"]
         if self.order == "mix":
             # one exponential between two other ops: fma k+2, exp k; packs and dots
@@ -277,9 +286,24 @@ class Gen:
                     f"v_add_f32 {vr(L.LS0)}, {vr(L.LS0)}, {vr(L.LS1)}"]
         return head + [
                 f"v_cmp_nge_f32 vcc, 0x43800000, {vr(L.LS0)}",    # !(256 >= ls): ls > 256 or NaN
-                f"s_branch {lbl('RSTUB_' + site)}" if self.always_rare else f"s_cbranch_vccnz {lbl('RSTUB_' + site)}",
+                ("s_nop 0" if self.no_rare else
+                 f"s_branch {lbl('RSTUB_' + site)}" if self.always_rare else f"s_cbranch_vccnz {lbl('RSTUB_' + site)}"),
                 f"{lbl('RRET_' + site)}:",
                 f"v_add_f32 {vr(L.VL)}, {vr(L.VL)}, {vr(L.LS0)}"]
+
+    def place_softmax(self, fill: dict[int, list[str]], S: int, P: int, slots: list[int], at: int,
+                      site: str, sset: str) -> None:
+        """The softmax of (S, P) spread over `slots`, its rare test and branch after
+        MFMA `at`.  With tail_split the compare ends the spread ops (one MFMA and its
+        operand reads before the branch, so the branch does not wait on it)."""
+        tail = self.softmax_tail(site, sset)
+        if self.tail_split:
+            k = next(i for i, x in enumerate(tail) if x.startswith("v_cmp_nge_f32"))
+            self.spread(self.softmax_ops(S, P) + tail[:k + 1], slots, fill)
+            fill.setdefault(at, []).extend(tail[k + 1:])
+        else:
+            self.spread(self.softmax_ops(S, P), slots, fill)
+            fill.setdefault(at, []).extend(tail)
 
     def mask_check(self, site: str, sset: str, desc: int, half: int) -> list[str]:
         if self.no_mask:
@@ -360,10 +384,11 @@ class Gen:
         moves the soffsets; a change of source (video <-> extra rows) calls SWITCH."""
         self.stubs += [f"{lbl('SWSTUB_' + site)}:", f"s_call_b64 {sr(S_RET, 2)}, {lbl('SWITCH')}",
                        f"s_branch {lbl('SWRET_' + site)}"]
-        r = [
-            f"s_lshr_b32 s74, {sr(x)}, 31",
-            f"s_cmp_lg_u32 s74, {sr(S_CUR)}",
-            f"s_cbranch_scc1 {lbl('SWSTUB_' + site)}",
+        # (no_switch keeps the check in the setup decodes, sites S0 / S1, which load
+        # the buffer resources of the first block's source)
+        chk = [] if (self.no_switch and not site.startswith("S")) else [
+            f"s_lshr_b32 s74, {sr(x)}, 31", f"s_cmp_lg_u32 s74, {sr(S_CUR)}", f"s_cbranch_scc1 {lbl('SWSTUB_' + site)}"]
+        r = chk + [
             f"{lbl('SWRET_' + site)}:",
             f"s_and_b32 s73, {sr(x)}, 0x7fffffff",
             "s_lshl_b32 s73, s73, 6",                                  # first row of the block
@@ -469,6 +494,8 @@ class Gen:
             if m[0] == "qk":
                 _, _, _, c, S = m
                 self.e(f"{self.mfma} {vr(S, 16)}, {vr(slot, 4)}, {vr(L.Q + 4 * c, 4)}, {'0' if c == 0 else vr(S, 16)}")
+                if self.qk_dup:
+                    self.e(f"{self.mfma} {vr(S, 16)}, {vr(slot, 4)}, {vr(L.Q + 4 * c, 4)}, {vr(S, 16)}")
             else:
                 _, _, st16, dt, P = m
                 acc = vr(L.O + 16 * dt, 16)
@@ -535,14 +562,12 @@ class Gen:
         sm = self.sm_start
         # sub-iteration a: softmax of sub-block 2j-1 (S_B, block j-1 half 1)
         fill.setdefault(sm - 1, []).extend(self.mask_check(site + "a", "B", S_ENT + 2 * vst + 1, 1))
-        self.spread(self.softmax_ops(L.SB, L.PB), list(range(sm, M - 1)), fill)
-        fill.setdefault(M - 1, []).extend(self.softmax_tail(site + "a", "B"))
+        self.place_softmax(fill, L.SB, L.PB, list(range(sm, M - 1)), M - 1, site + "a", "B")
         # sub-iteration b: softmax of sub-block 2j (S_A, block j half 0)
         if self.early_load:
             fill.setdefault(M, []).extend(self.entry_load(stage))
         fill.setdefault(M + sm - 1, []).extend(self.mask_check(site + "b", "A", S_ENT + 2 * stage + 1, 0))
-        self.spread(self.softmax_ops(L.SA, L.PA), list(range(M + sm, 2 * M - 1)), fill)
-        fill.setdefault(2 * M - 1, []).extend(self.softmax_tail(site + "b", "A"))
+        self.place_softmax(fill, L.SA, L.PA, list(range(M + sm, 2 * M - 1)), 2 * M - 1, site + "b", "A")
         lead = self.lead_pv(vst)
         self.stream(mf, fill, pre=len(lead), nxt=self.lead_pv(stage))
         self.iteration_tail(stage, load=not self.early_load)
@@ -556,8 +581,7 @@ class Gen:
         for k in range(2 * L.NCP):
             self.place_copy(fill, 1 + k, 2, k)
         fill.setdefault(L.NQK + 1, []).extend(self.mask_check("F", "A", S_ENT + 1, 0))
-        self.spread(self.softmax_ops(L.SA, L.PA), list(range(L.NQK + 2, 2 * L.NQK - 1)), fill)
-        fill.setdefault(2 * L.NQK - 1, []).extend(self.softmax_tail("F", "A"))
+        self.place_softmax(fill, L.SA, L.PA, list(range(L.NQK + 2, 2 * L.NQK - 1)), 2 * L.NQK - 1, "F", "A")
         self.stream(mf, fill, nxt=self.lead_pv(0))
         self.iteration_tail(0)
 
@@ -569,8 +593,7 @@ class Gen:
         mf = [("pv", stage, k // L.NDT, k % L.NDT, L.PA) for k in range(nh)] + \
              [("pv", stage, 2 + k // L.NDT, k % L.NDT, L.PB) for k in range(nh)]
         fill: dict[int, list[str]] = {0: self.mask_check(f"D{stage}", "B", S_ENT + 2 * stage + 1, 1)}
-        self.spread(self.softmax_ops(L.SB, L.PB), list(range(1, nh - 1)), fill)
-        fill.setdefault(nh - 1, []).extend(self.softmax_tail(f"D{stage}", "B"))
+        self.place_softmax(fill, L.SB, L.PB, list(range(1, nh - 1)), nh - 1, f"D{stage}", "B")
         self.stream(mf, fill)
         # the code after the asm reads O with VALU: 12 states after the last MFMA
         self.e("s_waitcnt vmcnt(0) lgkmcnt(0)", "s_nop 15", f"s_branch {lbl('END')}")
@@ -643,10 +666,14 @@ def operands(D: int, nw: int = 8, rs: bool = False) -> list[str]:
 # branch on the SCC of the mask test's s_and and set a copy's M0 one MFMA
 # slot early (together 0.6% on Wan 4x, CogVideoX neutral); both take the row
 # sums from two 16x16x32 MFMAs against a ones pattern instead of eight v_dot2
-# and an add per sub-block (Wan 4x 2.7%, CogVideoX 1.9%).  Measured neutral
-# and not used: the D = 64 softmax spread over one more MFMA slot (sm_start 1).
-PRODUCT = {128: dict(lead=2, early_load=True, dot_init=True, and_scc=True, copy_split=True, rs_mfma=True),
-           64: dict(dot_init=True, and_scc=True, copy_split=True, rs_mfma=True)}
+# and an add per sub-block (Wan 4x 2.7%, CogVideoX 1.9%), and issue the rare
+# test one MFMA before its branch (Wan 4x 1.2%, CogVideoX 0.6%).  Measured
+# neutral and not used: the D = 64 softmax spread over one more MFMA slot
+# (sm_start 1), one LDS wait per two MFMAs (wait_pair), 8 wait states before
+# the row sum is read (tail_nop 8).
+PRODUCT = {128: dict(lead=2, early_load=True, dot_init=True, and_scc=True, copy_split=True, rs_mfma=True,
+                     tail_split=True),
+           64: dict(dot_init=True, and_scc=True, copy_split=True, rs_mfma=True, tail_split=True)}
 
 
 def render(per_d: dict | None = None, **opts) -> str:
