@@ -153,7 +153,8 @@ class Gen:
                  lead: int = 0, early_load: bool = False, no_mask: bool = False, dot_init: bool = False,
                  and_scc: bool = False, copy_split: bool = False, sm_start: int = 2, rs_mfma: bool = False,
                  wait_pair: bool = False, rs_mix: bool = False, tail_nop: int = 12, no_switch: bool = False,
-                 no_fma: bool = False, qk_dup: bool = False, no_rare: bool = False, tail_split: bool = False):
+                 no_fma: bool = False, qk_dup: bool = False, no_rare: bool = False, tail_split: bool = False,
+                 mask_fast: bool = False):
         assert dt in ("bf16", "f16")
         self.dt = dt
         self.L = Layout(D, nw, rs=rs_mfma)
@@ -166,6 +167,7 @@ class Gen:
         self.qk_dup = qk_dup            # timing only (wrong results): every QK MFMA issued twice
         self.no_rare = no_rare          # timing only (wrong results): the rare-path branch never taken
         self.tail_split = tail_split    # rare test issued one MFMA before its branch
+        self.mask_fast = mask_fast      # MASK: one lane mask for all 16 keys when the key split lies outside
         self.pad = pad                  # diagnostics: 16 wait states after every MFMA
         self.always_rare = always_rare  # diagnostics: exact row max on every sub-block
         self.la = (LA if nw == 8 else 2) if la is None else la   # MFMAs of LDS operand lookahead
@@ -366,6 +368,19 @@ class Gen:
              "s_bitcmp1_b32 s90, 3", "s_cselect_b64 s[94:95], -1, 0", "s_and_b64 s[94:95], s[94:95], s[78:79]",
              "s_or_b64 s[82:83], s[92:93], s[94:95]",      # lanes whose hi keys are allowed
              f"v_sub_u32 {vr(L.VT)}, s88, {vr(L.H4)}"]      # kb - 32*half - 4h
+        if self.mask_fast:
+            # key split outside this sub-block: all its keys are lo (kb - 32*half >= 32)
+            # or all hi (<= 0), so one lane mask (the allowed part) covers every key,
+            # and a mask of all lanes needs nothing at all
+            lo, hi, one, ret = (lbl(name + x) for x in ("_LO", "_HI", "_ONE", "_RET"))
+            r += ["s_cmp_ge_i32 s88, 32", f"s_cbranch_scc1 {lo}", "s_cmp_le_i32 s88, 0", f"s_cbranch_scc1 {hi}"]
+            tail = [f"{lo}:", "s_mov_b64 s[84:85], s[80:81]", f"s_branch {one}",
+                    f"{hi}:", "s_mov_b64 s[84:85], s[82:83]",
+                    f"{one}:", "s_cmp_eq_u64 s[84:85], -1", f"s_cbranch_scc1 {ret}", "s_nop 0"]
+            tail += [f"v_cndmask_b32_e64 {vr(S + k)}, {vr(L.NEGINF)}, {vr(S + k)}, s[84:85]" for k in range(16)]
+            tail += [f"{ret}:", f"s_setpc_b64 {sr(S_RET, 2)}"]
+        else:
+            tail = []
         for k in range(16):
             ck = 8 * (k // 4) + (k % 4)
             r += [f"v_cmp_lt_i32 vcc, {ck}, {vr(L.VT)}",    # key below kb
@@ -375,7 +390,7 @@ class Gen:
                   "s_nop 0",
                   f"v_cndmask_b32_e64 {vr(S + k)}, {vr(L.NEGINF)}, {vr(S + k)}, s[84:85]"]
         r += [f"s_setpc_b64 {sr(S_RET, 2)}"]
-        return r
+        return r + tail
 
     # ── copies ──
     def decode(self, x: int, site: str) -> list[str]:
@@ -672,8 +687,8 @@ def operands(D: int, nw: int = 8, rs: bool = False) -> list[str]:
 # (sm_start 1), one LDS wait per two MFMAs (wait_pair), 8 wait states before
 # the row sum is read (tail_nop 8).
 PRODUCT = {128: dict(lead=2, early_load=True, dot_init=True, and_scc=True, copy_split=True, rs_mfma=True,
-                     tail_split=True),
-           64: dict(dot_init=True, and_scc=True, copy_split=True, rs_mfma=True, tail_split=True)}
+                     tail_split=True, mask_fast=True),
+           64: dict(dot_init=True, and_scc=True, copy_split=True, rs_mfma=True, tail_split=True, mask_fast=True)}
 
 
 def render(per_d: dict | None = None, **opts) -> str:

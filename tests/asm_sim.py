@@ -30,6 +30,10 @@ import gen_stream_asm as G  # noqa: E402
 M32 = 0xFFFFFFFF
 
 
+def i32(x):
+    return x - (1 << 32) if x & 0x80000000 else x
+
+
 def f2u(x):
     return np.asarray(x, dtype=np.float32).view(np.uint32)
 
@@ -238,6 +242,13 @@ class Wave:
             self.scc = int(self.sval(a[0]) < self.sval(a[1]))
         elif op == 's_cmp_ge_u32':
             self.scc = int(self.sval(a[0]) >= self.sval(a[1]))
+        elif op in ('s_cmp_ge_i32', 's_cmp_le_i32'):
+            x, y = (i32(self.sval(t)) for t in a[:2])
+            self.scc = int(x >= y if op == 's_cmp_ge_i32' else x <= y)
+        elif op == 's_cmp_eq_u64':
+            self.scc = int(self.sval64(a[0]) == self.sval64(a[1]))
+        elif op == 's_mov_b64':
+            self.sset64(a[0], self.sval64(a[1]))
         elif op == 's_bfe_u32':
             x, c = self.sval(a[1]), self.sval(a[2])
             off, wd = c & 31, (c >> 16) & 0x7F
