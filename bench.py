@@ -87,14 +87,16 @@ def copy_calibration(mib: int) -> int:
 
 
 def source_hash() -> str:
-    """Hash of the HIP sources and the build script: names the build a
-    committed counters file was measured on."""
+    """Hash of what is compiled (the HIP sources, headers, the generated key
+    loop and the build script): names the build a committed counters file was
+    measured on.  The loop generator itself is left out: its output, the
+    .inc, is hashed, so a comment in the generator does not rename the build."""
     import hashlib
 
     h = hashlib.sha256()
     pkg = os.path.join(ROOT, "longvideosparseattention_amd")
     csrc = os.path.join(pkg, "csrc")
-    files = sorted(f for f in os.listdir(csrc) if f.endswith((".hip", ".h", ".inc", ".py")))
+    files = sorted(f for f in os.listdir(csrc) if f.endswith((".hip", ".h", ".inc")))
     for name in files + ["../build_lib.py", "../../include/lvsa_amd.h"]:
         with open(os.path.join(csrc, name), "rb") as f:
             h.update(name.encode() + b"\0" + f.read())

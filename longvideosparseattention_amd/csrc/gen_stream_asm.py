@@ -681,8 +681,10 @@ def operands(D: int, nw: int = 8, rs: bool = False) -> list[str]:
 # branch on the SCC of the mask test's s_and and set a copy's M0 one MFMA
 # slot early (together 0.6% on Wan 4x, CogVideoX neutral); both take the row
 # sums from two 16x16x32 MFMAs against a ones pattern instead of eight v_dot2
-# and an add per sub-block (Wan 4x 2.7%, CogVideoX 1.9%), and issue the rare
-# test one MFMA before its branch (Wan 4x 1.2%, CogVideoX 0.6%).  Measured
+# and an add per sub-block (Wan 4x 2.7%, CogVideoX 1.9%), issue the rare
+# test one MFMA before its branch (Wan 4x 1.2%, CogVideoX 0.6%), and mask a
+# sub-block that lies on one side of the key split with one lane mask
+# (CogVideoX 1.0%, Wan 4x 0.25%).  Measured
 # neutral and not used: the D = 64 softmax spread over one more MFMA slot
 # (sm_start 1), one LDS wait per two MFMAs (wait_pair), 8 wait states before
 # the row sum is read (tail_nop 8).
