@@ -38,6 +38,7 @@ from longvideosparseattention_amd import hip_ops as lvops  # noqa: E402
 from longvideosparseattention_amd import flops as lvflops  # noqa: E402
 
 MFMA_BF16_PEAK_TFLOPS = 2500.0
+MFMA_PEAK_TFLOPS = {"bf16": 2500.0, "f16": 2500.0, "f32": 157.3}   # MI355X dense MFMA
 HBM_PEAK_GBS = 8000.0
 
 CONFIGS = {
@@ -66,6 +67,9 @@ def parse(argv=None):
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-baseline sample budget")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--dtype", choices=["bf16", "f16", "f32"], default=None,
+                    help="input dtype; default bf16, and f32 for the reference's CPU configuration, which is "
+                         "quoted in fp32 (fp32 inputs run the fp32 MFMA kernel)")
     ap.add_argument("--window", type=int, default=None,
                     help="override the configuration's sliding window (the Wan 6x sweep uses 1, 2, 4)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -212,7 +216,9 @@ def main(argv=None) -> int:
         W = args.window
         workload += f", window +-{W}"
     N = T * P
-    dt = torch.bfloat16
+    dname = args.dtype or ("f32" if args.config == "cpu" else "bf16")
+    dt = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[dname]
+    peak = MFMA_PEAK_TFLOPS[dname]
 
     # Synthetic inputs: one CPU generator, fp32 randn in order q, k, v, text q, k, v.
     g = torch.Generator().manual_seed(args.seed)
@@ -233,7 +239,7 @@ def main(argv=None) -> int:
         t0 = time.perf_counter()
         m = lv.LVSAMetadata.build(total_latent_frames=T, num_patches=P, window_size=W, n_first_frames=1,
                                   key_frame_interval=kfi, rank=0, world=1, keyframe_offset=off)
-        m.full_plan(dev, N, N, n_text, n_text, D)
+        m.full_plan(dev, N, N, n_text, n_text, D, dt)
         torch.cuda.synchronize()
         build_ms.append(1e3 * (time.perf_counter() - t0))
         metas[off] = m
@@ -270,10 +276,12 @@ def main(argv=None) -> int:
         D, "attn_fwd_kernel")
     if D in (64, 128) and os.environ.get("LVSA_ATTN_KERNEL") == "pp":
         kernel = "attn_fwd_pp_kernel"
+    if dname == "f32":
+        kernel = "attn_fwd_f32_kernel"
 
     line = {
-        "metric": "block-sparse attn ms/call + effective TFLOP/s (% bf16 MFMA peak), "
-                  + {"wan4x": "Wan 4x shape"}.get(args.config, args.config + " shape"),
+        "metric": f"block-sparse attn ms/call + effective TFLOP/s (% {'fp32' if dname == 'f32' else 'bf16'} "
+                  "MFMA peak), " + {"wan4x": "Wan 4x shape"}.get(args.config, args.config + " shape"),
         "value": round(value, 2),
         "unit": "TFLOP/s",
         "n_gpus": 1,
@@ -283,12 +291,13 @@ def main(argv=None) -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic: seeded N(0,1) q/k/v, bf16, RoPE-free; keyframe offset = step % kfi",
+        "dtype": dname,
+        "data": f"synthetic: seeded N(0,1) q/k/v, {dname}, RoPE-free; keyframe offset = step % kfi",
         "config": {"workload": workload, "T": T, "P": P, "heads": H, "head_dim": D, "window": W,
                    "kfi": kfi, "n_first": 1, "offsets": offsets, "text_tokens": n_text, "block": block,
                    "batch": 1, "parallelism": "single GPU"},
         "pct_bf16_mfma_peak": round(100 * value / MFMA_BF16_PEAK_TFLOPS, 2),
+        "pct_mfma_peak": round(100 * value / peak, 2),      # of the MFMA peak of the input dtype
         "tflops_token_exact": round(fx / wall / 1e12, 2),
         "gflop_per_call_block": round(fb / args.steps / 1e9, 1),
         "hbm_gbs_algorithmic": round(bytes_per_call / (ms * 1e-3) / 1e9, 1),
@@ -299,8 +308,8 @@ def main(argv=None) -> int:
         # achieved = block FLOPs / the HIP-event span of the timed calls on the
         # launch stream (the attention kernel, plus the text merge kernel
         # where text tiles are split); rocprof kernel averages: profiles/
-        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": traffic,
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak,
+                     "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": traffic,
                      "traffic_source": traffic_src, "traffic_note": traffic_note, "kernel": kernel,
                      "event_ms_per_call": round(ev_ms, 4), "build": source_hash()},
     }
