@@ -24,7 +24,10 @@ otherwise.
 from __future__ import annotations
 
 import math
+import os
 import sys
+import threading
+from collections import OrderedDict
 from dataclasses import dataclass, field
 from typing import Any, Dict, Iterator, List, Optional, Set, Tuple
 
@@ -203,6 +206,29 @@ class _DeviceState:
     plans: Dict[Tuple, hip_ops.BlockPlan] = field(default_factory=dict)
 
 
+# Patterns built by LVSAMetadata.build, shared by every caller that asks for
+# the same one.  The reference's plugin hooks (``attention_impl.py:387-419``,
+# ``hunyuan_hook.py:185-215``) keep one pattern per attention layer and rebuild
+# it at every denoising step; with the cache the layers of a step share one
+# build, one device mask and one set of block plans.
+_BUILD_CACHE: "OrderedDict[tuple, LVSAMetadata]" = OrderedDict()
+_BUILD_LOCK = threading.Lock()
+
+
+def _build_cache_size() -> int:
+    """Patterns kept (LRU): ``LVSA_METADATA_CACHE``, default 16; 0 turns the cache off."""
+    try:
+        return max(0, int(os.environ.get("LVSA_METADATA_CACHE", "16")))
+    except ValueError:
+        return 16
+
+
+def clear_metadata_cache() -> None:
+    """Drop every cached pattern (and with it, once unreferenced, its device mask and plans)."""
+    with _BUILD_LOCK:
+        _BUILD_CACHE.clear()
+
+
 @dataclass
 class LVSAMetadata:
     """Pre-computed sparse attention pattern (``lvsa/sparse_attention.py:286-333``).
@@ -212,6 +238,10 @@ class LVSAMetadata:
     they are produced by the ``lvsa_mask_build`` kernel on first use on a
     device (``ensure_device`` or any attention call) and returned as device
     int32 tensors.
+
+    ``build`` returns one shared instance per set of pattern arguments (and
+    current GPU), so an instance is read-only, as the reference's callers
+    treat it.
     """
 
     # ── Pattern config ──
@@ -275,7 +305,36 @@ class LVSAMetadata:
         ``key_frame_interval`` is used verbatim (callers wanting auto-scaling
         call ``compute_auto_kfi`` first); ``reference_frames`` and
         ``sparsity_scale`` are accepted for signature compatibility.
+
+        Repeated arguments return the instance built first (an LRU of
+        ``LVSA_METADATA_CACHE`` patterns, default 16, keyed also by the current
+        GPU), with the device mask and plans it has already built.
         """
+        guards_key = tuple(sorted(set(boundary_guards or [])))
+        dev = torch.cuda.current_device() if torch.cuda.is_available() else -1
+        key = (total_latent_frames, num_patches, window_size, n_first_frames, key_frame_interval, rank, world,
+               bool(expand_window), keyframe_offset, guards_key, dev)
+        size = _build_cache_size()
+        if size:
+            with _BUILD_LOCK:
+                hit = _BUILD_CACHE.get(key)
+                if hit is not None:
+                    _BUILD_CACHE.move_to_end(key)
+                    return hit
+        m = cls._build(total_latent_frames, num_patches, window_size, n_first_frames, key_frame_interval, rank,
+                       world, expand_window, keyframe_offset, boundary_guards)
+        if size:
+            with _BUILD_LOCK:
+                m = _BUILD_CACHE.setdefault(key, m)
+                _BUILD_CACHE.move_to_end(key)
+                while len(_BUILD_CACHE) > size:
+                    _BUILD_CACHE.popitem(last=False)
+        return m
+
+    @classmethod
+    def _build(cls, total_latent_frames: int, num_patches: int, window_size: int, n_first_frames: int,
+               key_frame_interval: Optional[int], rank: int, world: int, expand_window: bool,
+               keyframe_offset: int, boundary_guards: Optional[List[int]]) -> "LVSAMetadata":
         T, P, W = total_latent_frames, num_patches, window_size
         total_seq = T * P
         assert total_seq % world == 0, (

@@ -217,3 +217,30 @@ def test_shim_binds_the_reference_import_names():
     root = str(__import__("pathlib").Path(__file__).resolve().parents[1])
     res = subprocess.run([sys.executable, "-c", code], cwd=root, capture_output=True, text=True, timeout=300)
     assert res.returncode == 0 and res.stdout.strip().endswith("ok"), res.stderr[-2000:]
+
+
+def test_build_returns_one_shared_pattern_per_argument_set(monkeypatch):
+    """The plugin hooks rebuild the pattern in every layer at every step
+    (attention_impl.py:387-419): repeated arguments return the instance built
+    first, LRU-bounded by LVSA_METADATA_CACHE (0 turns the cache off)."""
+    sa.clear_metadata_cache()
+    kw = dict(total_latent_frames=9, num_patches=256, window_size=1, n_first_frames=1, key_frame_interval=4,
+              rank=0, world=1)
+    a = lv.LVSAMetadata.build(keyframe_offset=3, **kw)
+    # reference_frames / sparsity_scale do not enter the pattern (kfi is used verbatim)
+    assert lv.LVSAMetadata.build(keyframe_offset=3, reference_frames=7, sparsity_scale=2.0, **kw) is a
+    b = lv.LVSAMetadata.build(keyframe_offset=2, **kw)
+    assert b is not a and b.global_indices == [0, 1, 2, 6] and a.global_indices == [0, 2, 3, 7]
+    assert lv.LVSAMetadata.build(keyframe_offset=3, boundary_guards=[5], **kw) is not a
+    assert lv.LVSAMetadata.build(keyframe_offset=3, expand_window=False, **kw) is not a
+
+    monkeypatch.setenv("LVSA_METADATA_CACHE", "2")
+    sa.clear_metadata_cache()
+    ms = [lv.LVSAMetadata.build(keyframe_offset=o, **kw) for o in range(3)]
+    assert lv.LVSAMetadata.build(keyframe_offset=2, **kw) is ms[2]
+    assert lv.LVSAMetadata.build(keyframe_offset=0, **kw) is not ms[0]      # evicted (LRU of 2)
+
+    monkeypatch.setenv("LVSA_METADATA_CACHE", "0")
+    x, y = (lv.LVSAMetadata.build(keyframe_offset=1, **kw) for _ in range(2))
+    assert x is not y and x.global_indices == y.global_indices
+    sa.clear_metadata_cache()

@@ -179,10 +179,12 @@ class TestDynamicReconfiguration:
         p.set_sparsity_scale(0.5)
         assert p._metadata is m
 
-    def test_pattern_cache_keeps_two_parameter_sets(self):
+    def test_pattern_cache_keeps_two_parameter_sets(self, monkeypatch):
         """Patterns of at most the current and the previous (window, kfi,
         sparsity) set stay cached; switching back to the previous set reuses
-        its metadata, older sets are dropped."""
+        its metadata, older sets are dropped.  (The process-wide cache of
+        LVSAMetadata.build is off here, so a dropped set is built anew.)"""
+        monkeypatch.setenv("LVSA_METADATA_CACHE", "0")
         p = _proc(T=81, W=3, n_first=1, kfi=None)
         for scale in (0.5, 0.7, 0.9, 1.3, 0.5):
             p.set_sparsity_scale(scale)
