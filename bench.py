@@ -72,6 +72,8 @@ def parse(argv=None):
                          "quoted in fp32 (fp32 inputs run the fp32 MFMA kernel)")
     ap.add_argument("--window", type=int, default=None,
                     help="override the configuration's sliding window (the Wan 6x sweep uses 1, 2, 4)")
+    ap.add_argument("--head-dim", type=int, default=None, choices=[64, 96, 128, 192, 256],
+                    help="override the configuration's head size (the plugin's head sizes, same geometry)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="instead of the benchmark, copy a MIB-MiB device buffer 4 times (one kernel each): "
                          "the known-size reference that scales rocprof FETCH_SIZE / WRITE_SIZE to bytes")
@@ -215,6 +217,9 @@ def main(argv=None) -> int:
     if args.window is not None:
         W = args.window
         workload += f", window +-{W}"
+    if args.head_dim is not None and args.head_dim != D:
+        D = args.head_dim
+        workload += f", head size {D}"
     N = T * P
     dname = args.dtype or ("f32" if args.config == "cpu" else "bf16")
     dt = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[dname]
@@ -270,11 +275,12 @@ def main(argv=None) -> int:
     value = fb / wall / 1e12
     achieved = fb / (ev_ms * 1e-3 * args.steps) / 1e12
     bytes_per_call = 4 * (N + n_text) * H * D * 2
-    traffic, traffic_src, traffic_note = profiled_traffic(args.config if args.window is None else
-                                                          f"{args.config}_w{W}")
-    kernel = {128: "attn_fwd_stream_kernel", 64: "attn_fwd_stream_kernel", 96: "attn_fwd_pp_kernel"}.get(
+    tag = args.config + ("" if args.window is None else f"_w{W}") + (
+        "" if args.head_dim is None or args.head_dim == CONFIGS[args.config][3] else f"_d{D}")
+    traffic, traffic_src, traffic_note = profiled_traffic(tag)
+    kernel = {128: "attn_fwd_stream_kernel", 64: "attn_fwd_stream_kernel", 96: "attn_fwd_stream_kernel"}.get(
         D, "attn_fwd_kernel")
-    if D in (64, 128) and os.environ.get("LVSA_ATTN_KERNEL") == "pp":
+    if D in (64, 96, 128) and os.environ.get("LVSA_ATTN_KERNEL") == "pp":
         kernel = "attn_fwd_pp_kernel"
     if dname == "f32":
         kernel = "attn_fwd_f32_kernel"

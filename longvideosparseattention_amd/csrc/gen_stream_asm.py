@@ -1,4 +1,4 @@
-"""Generate the key loop of the single-stream attention kernel (D = 64 and 128).
+"""Generate the key loop of the single-stream attention kernel (D = 64, 96 and 128).
 
     python gen_stream_asm.py [out.inc]   (default: lvsa_attn_stream_body.inc beside this file)
 
@@ -56,6 +56,9 @@ Register map (VGPRs; the kernel's operands pin them), D = 128 (D = 64):
   rs_mfma the two partial row sums give way to a ones pattern and a row-sum
   tile (4 each).  The 12-wave D = 64 map (Layout nw = 12) has four operand
   slots, eight softmax temps and the RARE temps inside them: 148 VGPRs.
+  D = 96 (6 k-steps, 3 d-tiles) follows the D = 128 map with fewer O, Q and
+  offset registers (202 VGPRs) and uses the D = 128 LDS layout: 256-byte rows
+  whose chunks 12-15 the copies fill with zeros and no read touches.
 SGPRs: s[20:21] entry pointer, s22 blocks, s23 scale*log2(e), s[24:31] K/V
 bases (video, extra), s32-35 row strides, s36-37 source lengths, s38 wave,
 s39 LDS copy base of the wave; s40-s95 scratch.
@@ -87,7 +90,7 @@ class Layout:
     rare path's temporaries shared with them."""
 
     def __init__(self, D: int, nw: int = 8, rs: bool = False):
-        assert D in (64, 128) and nw in (8, 12) and (nw == 8 or D == 64)
+        assert D in (64, 96, 128) and nw in (8, 12) and (nw == 8 or D == 64)
         self.D = D
         self.nw = nw
         self.rs = rs                      # row sums by MFMA: ONES (A pattern) and RS (result) tiles
@@ -95,10 +98,12 @@ class Layout:
         self.NT = 16 if nw == 8 else 8       # softmax temporaries
         self.NQK = D // 16                # MFMA k-steps of a score tile
         self.NDT = D // 32                # 32-wide d-tiles of O
-        self.RB = 2 * D                   # bytes per K/V row in LDS
+        # D = 96 rows sit on the D = 128 LDS pitch: chunks 12-15 of a row are
+        # filled by copy lanes reading out of range (zeros) and never read
+        self.RB = 2 * (128 if D == 96 else D)   # bytes per K/V row in LDS
         self.TILE = 64 * self.RB          # one K or V block
         self.VBASE = 4 * self.TILE        # V stages follow the 4 K stages
-        self.NCP = D // 64                # 1 KiB copies of K (and of V) per wave and block
+        self.NCP = self.RB // 128         # 1 KiB copies of K (and of V) per wave and block
         r = 0
 
         def take(n: int) -> int:
@@ -187,6 +192,7 @@ class Gen:
         self.sm_start = sm_start        # first MFMA slot of a sub-iteration's softmax (mask test one before)
         self.lines: list[str] = []
         self.stubs: list[str] = []
+        self.phase = 0                  # operand slot of the next stream's first MFMA
 
     def e(self, *ins: str) -> None:
         self.lines.extend(ins)
@@ -481,7 +487,7 @@ class Gen:
 
         def reads(i: int) -> list[str]:
             m = seq[i]
-            slot = L.OPS + 4 * (i % L.nslot)
+            slot = slot_of(i)
             if m[0] == "qk":
                 _, st, half, c, _ = m
                 return [f"ds_read_b128 {vr(slot, 4)}, {vr(L.KOFF + c)} offset:{st * L.TILE + half * 32 * L.RB}"]
@@ -491,6 +497,11 @@ class Gen:
                 return [f"ds_read_b128 {vr(slot, 4)}, {vr(L.KOFF + dt)} offset:{off}"]
             return [f"ds_read_b64_tr_b16 {vr(slot, 2)}, {vr(L.VOFFA + dt)} offset:{off}",
                     f"ds_read_b64_tr_b16 {vr(slot + 2, 2)}, {vr(L.VOFFB + dt)} offset:{off}"]
+
+        ph = self.phase
+
+        def slot_of(i: int) -> int:
+            return L.OPS + 4 * ((ph + i) % L.nslot)
 
         issued = min(LA + pre, n)
         for i in range(pre, issued):
@@ -505,7 +516,7 @@ class Gen:
                 pending = sum(nreads[j] for j in range(last + 1, issued))
                 self.e(f"s_waitcnt lgkmcnt({min(15, pending)})")
             m = mfmas[i]
-            slot = L.OPS + 4 * (i % L.nslot)
+            slot = slot_of(i)
             if m[0] == "qk":
                 _, _, _, c, S = m
                 self.e(f"{self.mfma} {vr(S, 16)}, {vr(slot, 4)}, {vr(L.Q + 4 * c, 4)}, {'0' if c == 0 else vr(S, 16)}")
@@ -524,6 +535,8 @@ class Gen:
         while issued < nn:                # the next stream's operands not yet read
             self.e(*reads(issued))
             issued += 1
+        # the next stream's MFMA k takes the slot this one gave item n + k
+        self.phase = (ph + n) % L.nslot
 
     @staticmethod
     def spread(ops: list[str], slots: list[int], fill: dict[int, list[str]]) -> None:
@@ -571,7 +584,8 @@ class Gen:
                     mf.append(pvs[lead + c])
         assert mf[:len(self.lead_pv(vst))] == self.lead_pv(vst)
         fill: dict[int, list[str]] = {0: [] if self.no_decode else self.decode(S_ENT + 2 * cst, site)}
-        at_copy = (6, 10, 22, 26) if L.NCP == 2 else (5, 13)
+        # copies after MFMAs spread over the block's 4*NQK MFMAs
+        at_copy = {8: (6, 10, 22, 26), 6: (4, 8, 16, 20), 4: (5, 13)}[L.NQK]
         for k, at in enumerate(at_copy):
             self.place_copy(fill, at, cst, k)
         sm = self.sm_start
@@ -637,7 +651,9 @@ class Gen:
         for stage in (1, 2, 3, 0):
             self.iteration(stage)
         e(f"s_branch {lbl('LOOP')}")
+        loop_phase = self.phase           # every iteration ends at the same slot phase
         for stage in range(4):
+            self.phase = loop_phase
             self.drain(stage)
         e(*self.stubs)
         e(*self.rare_routine(L.SA, L.PA, "RARE_A"), *self.rare_routine(L.SB, L.PB, "RARE_B"),
@@ -658,7 +674,11 @@ def operands(D: int, nw: int = 8, rs: bool = False) -> list[str]:
     os_ = ", ".join(f"o{t}" for t in range(L.NDT))
     outs = ", ".join(f'"+{{{vr(L.O + 16 * t, 16)}}}"(o{t})' for t in range(L.NDT))
     outs += f', "+{{{vr(L.VM, 2)}}}"(ml), "+{{{vr(L.ROW, 4)}}}"(misc)'
-    ins = (f'"{{{vr(L.Q, 4 * L.NQK)}}}"(qv), "{{{vr(L.KOFF, L.NQK)}}}"(koff), '
+    if 4 * L.NQK == 24:   # no 24-register operand class: Q as 16 + 8 registers (qv.lo, qv.hi)
+        q = f'"{{{vr(L.Q, 16)}}}"(qv.lo), "{{{vr(L.Q + 16, 8)}}}"(qv.hi)'
+    else:
+        q = f'"{{{vr(L.Q, 4 * L.NQK)}}}"(qv)'
+    ins = (f'{q}, "{{{vr(L.KOFF, L.NQK)}}}"(koff), '
            f'"{{{vr(L.VOFFA, 2 * L.NDT)}}}"(voff), "{{{vr(L.DMAROW, 2)}}}"(dma), '
            f'"{{s[20:23]}}"(sa), "{{s[24:31]}}"(sb), "{{s[32:39]}}"(sc)')
     if L.rs:
@@ -690,6 +710,8 @@ def operands(D: int, nw: int = 8, rs: bool = False) -> list[str]:
 # the row sum is read (tail_nop 8).
 PRODUCT = {128: dict(lead=2, early_load=True, dot_init=True, and_scc=True, copy_split=True, rs_mfma=True,
                      tail_split=True, mask_fast=True),
+           96: dict(lead=2, early_load=True, dot_init=True, and_scc=True, copy_split=True, rs_mfma=True,
+                    tail_split=True, mask_fast=True),
            64: dict(dot_init=True, and_scc=True, copy_split=True, rs_mfma=True, tail_split=True, mask_fast=True)}
 
 
@@ -698,7 +720,7 @@ def render(per_d: dict | None = None, **opts) -> str:
            "// attn_fwd_stream_kernel (lvsa_attn_stream.h) and their asm operand lists.",
            "// Do not edit; regenerate.",
            "#pragma once", ""]
-    for D, nw in ((128, 8), (64, 8), (64, 12)):
+    for D, nw in ((128, 8), (96, 8), (64, 8), (64, 12)):
         pf = prefix(D, nw)
         for dt, name in (("bf16", f"{pf}_LOOP_BF16"), ("f16", f"{pf}_LOOP_F16")):
             o = {**PRODUCT[D], **opts, **(per_d or {}).get(D, {})}

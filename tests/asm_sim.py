@@ -299,7 +299,7 @@ class Wave:
             so = self.sval(a[2])
             lds = self.sim.lds
             for ln in range(64):
-                off = int(vo[ln]) + so
+                off = (int(vo[ln]) + so) & M32       # 32-bit offset arithmetic
                 dst = self.m0 + 16 * ln
                 for dw in range(4):
                     o = off + 4 * dw

@@ -25,8 +25,9 @@ def test_committed_loop_is_generated():
 
 
 def _swz(r, D=128):
-    """16-byte chunk swizzle of LDS row r (lvsa_attn_kernels.h swz<D>)."""
-    if D == 128:
+    """16-byte chunk swizzle of LDS row r (lvsa_attn_kernels.h swz<D>; D = 96
+    rows use the D = 128 layout)."""
+    if D in (96, 128):
         return ((r & 3) << 2) | ((r >> 2) & 3)
     return (((r >> 1) & 1) << 2) | (((r >> 2) & 1) << 1) | ((r >> 3) & 1)
 
@@ -53,7 +54,8 @@ def run_loop(entries, nk, n_x, seed=0, dt="bf16", D=128, nw=8, **opts):
     rng = np.random.default_rng(seed)
     R = 32 * nw
     L = A.G.Layout(D, nw, rs=opts.get("rs_mfma", A.G.PRODUCT[D].get("rs_mfma", False)))
-    RB, NCH = 2 * D, D // 8
+    RB, NCH = L.RB, L.RB // 16            # LDS row pitch (D = 96: the D = 128 pitch), chunks per row
+    GRB = 2 * D                           # global row stride of K and V
     rnd = (lambda x: A.bf16_to_f32(A.bf16_round(x))) if dt == "bf16" else (lambda x: x.astype(np.float16).astype(np.float32))
     enc = (lambda x: A.bf16_round(x).astype(np.uint16).tobytes()) if dt == "bf16" else (lambda x: x.astype(np.float16).tobytes())
     q = rnd(rng.standard_normal((R, D)).astype(np.float32))
@@ -89,6 +91,8 @@ def run_loop(entries, nk, n_x, seed=0, dt="bf16", D=128, nw=8, **opts):
         crow = (w % 8) * (1024 // RB) + lane // NCH
         V[L.DMAROW] = crow
         V[L.C16] = ((lane % NCH) ^ np.array([_swz(x & 15, D) for x in crow])) * 16
+        if D == 96:   # chunks past the row's data: an offset beyond every source (zeros, no access)
+            V[L.C16] = np.where(V[L.C16] >= 16 * 12, 0x7FFF0000, V[L.C16])
         V[L.ROW], V[L.H4], V[L.NEGINF], V[L.VT] = 32 * w + i32, 4 * h, 0xFF800000, 0
         V[L.VM] = A.f2u(np.full(64, -1e30, np.float32))
         if L.rs:
@@ -100,7 +104,7 @@ def run_loop(entries, nk, n_x, seed=0, dt="bf16", D=128, nw=8, **opts):
         S[23] = int(A.f2u(np.float32(scale * 1.4426950408889634)))
         for i, b in enumerate((kb0, vb0, kb1, vb1)):
             S[24 + 2 * i], S[25 + 2 * i] = b & 0xFFFFFFFF, b >> 32
-        S[32:36] = [RB, RB, RB, RB]
+        S[32:36] = [GRB, GRB, GRB, GRB]
         S[36], S[37], S[38], S[39] = nk, n_x, w, 1024 * (w % 8)
         waves.append(W)
     sim.run(waves)
@@ -149,15 +153,16 @@ CASES = {
 }
 
 
-@pytest.mark.parametrize("D", [128, 64])
+@pytest.mark.parametrize("D", [128, 64, 96])
 @pytest.mark.parametrize("case", sorted(CASES))
 def test_loop_matches_attention(case, D):
     make, nk, n_x = CASES[case]
     entries = make()
     err, lse_err, copies = run_loop(entries, nk, n_x, D=D)
     assert err <= 4e-3 and lse_err <= 2e-3, (case, err, lse_err)
-    # D/32 copies per wave per block for blocks 0..n+1 (the last two repeat block n-1)
-    assert copies == 8 * (D // 32) * (len(entries) + 2)
+    # 2 * NCP copies (K and V) per wave per block for blocks 0..n+1 (the last
+    # two repeat block n-1); D = 96 copies whole D = 128 rows
+    assert copies == 8 * 2 * A.G.Layout(D).NCP * (len(entries) + 2)
 
 
 @pytest.mark.parametrize("case", sorted(CASES))
@@ -183,7 +188,7 @@ def test_loop_12_waves_row_split_past_255_and_rare_path():
     assert err <= 2e-3 and lse_err <= 2e-3, (err, lse_err)
 
 
-@pytest.mark.parametrize("D", [128, 64])
+@pytest.mark.parametrize("D", [128, 64, 96])
 def test_loop_rare_path_every_sub_block(D):
     """The exact-max path (rescale of O and l) on every sub-block gives the
     same attention."""
@@ -191,7 +196,7 @@ def test_loop_rare_path_every_sub_block(D):
     assert err <= 4e-3 and lse_err <= 2e-3
 
 
-@pytest.mark.parametrize("D", [128, 64])
+@pytest.mark.parametrize("D", [128, 64, 96])
 def test_loop_fp16(D):
     err, lse_err, _ = run_loop([(j, _tail(150, j)) for j in range(3)], 150, 0, seed=4, dt="f16", D=D)
     assert err <= 2e-3 and lse_err <= 2e-3
