@@ -159,7 +159,7 @@ class Gen:
                  and_scc: bool = False, copy_split: bool = False, sm_start: int = 2, rs_mfma: bool = False,
                  wait_pair: bool = False, rs_mix: bool = False, tail_nop: int = 12, no_switch: bool = False,
                  no_fma: bool = False, qk_dup: bool = False, no_rare: bool = False, tail_split: bool = False,
-                 mask_fast: bool = False):
+                 mask_fast: bool = False, mfma_order: str = "alt"):
         assert dt in ("bf16", "f16")
         self.dt = dt
         self.L = Layout(D, nw, rs=rs_mfma)
@@ -173,6 +173,7 @@ class Gen:
         self.no_rare = no_rare          # timing only (wrong results): the rare-path branch never taken
         self.tail_split = tail_split    # rare test issued one MFMA before its branch
         self.mask_fast = mask_fast      # MASK: one lane mask for all 16 keys when the key split lies outside
+        self.mfma_order = mfma_order    # QK / PV order in a sub-iteration: alternate, in pairs, or grouped
         self.pad = pad                  # diagnostics: 16 wait states after every MFMA
         self.always_rare = always_rare  # diagnostics: exact row max on every sub-block
         self.la = (LA if nw == 8 else 2) if la is None else la   # MFMAs of LDS operand lookahead
@@ -578,10 +579,14 @@ class Gen:
             pvs = [("pv", vst, 2 * half + c // half_q, c % L.NDT, P) for c in range(L.NQK)]
             lead = len(self.lead_pv(vst)) if half == 0 else 0
             mf += pvs[:lead]
-            for c in range(L.NQK):
-                mf.append(qks[c])
-                if lead + c < L.NQK:
-                    mf.append(pvs[lead + c])
+            rest = pvs[lead:]
+            if self.mfma_order == "group":
+                mf += qks + rest
+                continue
+            step = 2 if self.mfma_order == "pair" else 1
+            for c in range(0, L.NQK, step):
+                mf += qks[c:c + step] + rest[c:c + step]
+            mf += rest[L.NQK:]
         assert mf[:len(self.lead_pv(vst))] == self.lead_pv(vst)
         fill: dict[int, list[str]] = {0: [] if self.no_decode else self.decode(S_ENT + 2 * cst, site)}
         # copies after MFMAs spread over the block's 4*NQK MFMAs
@@ -707,7 +712,8 @@ def operands(D: int, nw: int = 8, rs: bool = False) -> list[str]:
 # (CogVideoX 1.0%, Wan 4x 0.25%).  Measured
 # neutral and not used: the D = 64 softmax spread over one more MFMA slot
 # (sm_start 1), one LDS wait per two MFMAs (wait_pair), 8 wait states before
-# the row sum is read (tail_nop 8).
+# the row sum is read (tail_nop 8), QK / PV MFMAs in pairs or grouped
+# (mfma_order).
 PRODUCT = {128: dict(lead=2, early_load=True, dot_init=True, and_scc=True, copy_split=True, rs_mfma=True,
                      tail_split=True, mask_fast=True),
            96: dict(lead=2, early_load=True, dot_init=True, and_scc=True, copy_split=True, rs_mfma=True,
