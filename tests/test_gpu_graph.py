@@ -21,17 +21,17 @@ from longvideosparseattention_amd import hip_ops
 
 pytestmark = pytest.mark.gpu
 
-T, P, H, NT = 12, 128, 4, 64
+T, H, NT = 12, 4, 64
 W, N_FIRST, KFI = 2, 1, 4
 
 
 def _step(meta, q, k, v, qt, kt, vt):
     """Mask, plan and attention for one offset: the device work of a step."""
-    D = q.shape[-1]
+    D, P = q.shape[-1], meta.num_patches
     dm = hip_ops.mask_build(meta._mask_params(), q.device)
     plan = hip_ops.plan_build(dm.rel_full, n_q=q.shape[1], n_k=k.shape[1], n_x=kt.shape[1], n_tq=qt.shape[1],
                               R=P, Cf=P, max_row_frames=max(1, meta.max_row_frames),
-                              block_q=hip_ops.attn_block_q(D))
+                              block_q=hip_ops.attn_block_q(D, q.dtype, P, P))
     o, ot, lse, lse_t = hip_ops.attn_fwd(q, k, v, plan, kx=kt, vx=vt, qt=qt, return_lse=True)
     return dict(frame_indptr=dm.frame_indptr, frame_indices=dm.frame_indices,
                 tile_indptr=plan.tile_indptr, entries=plan.entries, o=o, ot=ot, lse=lse, lse_t=lse_t)
@@ -50,8 +50,13 @@ def _assert_same(a, b, what):
         assert torch.equal(a[key], b[key]), (what, key)
 
 
-@pytest.mark.parametrize("D,offset", [(128, 0), (128, 3), (64, 1), (96, 2), (192, 3), (256, 0)])
-def test_step_graph_replays_match_eager(D, offset):
+# 128-token frames run the ping-pong / 4-wave kernels; 400-token frames the
+# single-stream kernels (D = 128 and 96 on 256-row tiles, D = 64 on 384-row
+# tiles with 12 waves), whose work-queue counters are zeroed by a kernel in
+# the captured graph.
+@pytest.mark.parametrize("D,offset,P", [(128, 0, 128), (128, 3, 128), (64, 1, 128), (96, 2, 128), (192, 3, 128),
+                                        (256, 0, 128), (128, 1, 400), (96, 3, 400), (64, 2, 400)])
+def test_step_graph_replays_match_eager(D, offset, P):
     dev = torch.device("cuda", 0)
     meta = lv.LVSAMetadata.build(total_latent_frames=T, num_patches=P, window_size=W, n_first_frames=N_FIRST,
                                  key_frame_interval=KFI, rank=0, world=1, keyframe_offset=offset)
