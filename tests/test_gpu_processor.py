@@ -88,10 +88,13 @@ def _rows(proc):
     return [set(r) for r in m.rows]
 
 
+# 96-token frames run the ping-pong / 4-wave kernels, 320-token frames the
+# single-stream kernels (D = 64, 96, 128)
+@pytest.mark.parametrize("P", [96, 320])
 @pytest.mark.parametrize("D", [64, 96, 128, 192])
 @pytest.mark.parametrize("n_txt", [0, 24], ids=["video", "dual_stream"])
-def test_call_matches_oracle_across_steps(n_txt, D, gpu):
-    T, P, W, n, kfi, H = 13, 96, 1, 1, 4, 2
+def test_call_matches_oracle_across_steps(n_txt, D, P, gpu):
+    T, W, n, kfi, H = 13, 1, 1, 4, 2
     ad = ReshapeAdapter(H, D)
     proc = _proc(T, P, W, n, kfi, ad)
     hid, enc = _draw([(1, T * P, 3 * H * D), (1, n_txt, 3 * H * D)])

@@ -18,7 +18,7 @@ from oracle import lvsa_mask as om
 
 pytestmark = pytest.mark.gpu
 
-T, P, H = 10, 128, 4
+T, H = 10, 4
 W, N_FIRST, KFI = 2, 1, 4
 
 
@@ -27,9 +27,12 @@ def _draw(shapes, seed):
     return [torch.randn(s, generator=g).to(torch.bfloat16) for s in shapes]
 
 
+# 128-token frames: the ping-pong kernel; 400-token frames: the single-stream
+# kernels (D = 128 on 256-row tiles, D = 64 on 384-row tiles)
+@pytest.mark.parametrize("P", [128, 400])
 @pytest.mark.parametrize("D", [128, 64])
 @pytest.mark.parametrize("n_txt", [48, 0])
-def test_compiled_steps_match_eager(n_txt, D):
+def test_compiled_steps_match_eager(n_txt, D, P):
     dev = torch.device("cuda", 0)
     N = T * P
     q, k, v, qt, kt, vt = (x.to(dev) for x in _draw(
@@ -70,7 +73,7 @@ def test_compiled_steps_match_eager(n_txt, D):
 
 def test_step_must_be_cpu_scalar():
     dev = torch.device("cuda", 0)
-    D = 128
+    D, P = 128, 128
     q = torch.zeros(1, T * P, H, D, dtype=torch.bfloat16, device=dev)
     z = torch.zeros(1, 0, H, D, dtype=torch.bfloat16, device=dev)
     with pytest.raises(ValueError, match="CPU"):
