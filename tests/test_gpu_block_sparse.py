@@ -38,11 +38,13 @@ def _csr(n_qblocks, n_kblocks, empty, g):
     return rows, indptr, indices
 
 
-@pytest.mark.parametrize("block_q", [128, 256])
+# R, C = 96, 80: generic descriptors, the ping-pong / 4-wave kernels;
+# R, C = 320, 300 (block_q 256): the single-stream kernels
+@pytest.mark.parametrize("block_q,R,C", [(128, 96, 80), (256, 96, 80), (256, 320, 300)])
 @pytest.mark.parametrize("D", [64, 96, 128, 192, 256])
-def test_arbitrary_csr_with_empty_rows(D, block_q, gpu, monkeypatch):
+def test_arbitrary_csr_with_empty_rows(D, block_q, R, C, gpu, monkeypatch):
     monkeypatch.setenv("LVSA_ATTN_BLOCK_Q", str(block_q))
-    R, C, H, HKV = 96, 80, 4, 2
+    H, HKV = 4, 2
     MB, NB = 7, 9
     M, N = MB * R, NB * C
     g = torch.Generator().manual_seed(D + block_q)
