@@ -76,6 +76,7 @@ S_KRS0, S_VRS0, S_KRS1, S_VRS1, S_NK, S_NX, S_WAVE, S_LDSK = 32, 33, 34, 35, 36,
 S_J, S_NM1, S_CUR, S_ENT, S_RK, S_RV = 40, 41, 42, 44, 52, 56
 S_SOK, S_SOV, S_KRSC = 60, 62, 64  # copy soffsets (K: 60, 61; V: 62, 63); strides, 32-row strides
 S_RET = 76
+S_SOVW, S_CURV = 68, 72            # wide map: V soffsets (68-71) and V's key source
 S_ONE = 43                         # a pair of 1.0 in the element type (row-sum dots)
 CLOBBER_S = list(range(40, 96))
 NSLOT = 8                         # LDS operand slots
@@ -87,30 +88,35 @@ class Layout:
     """Head-size dependent shapes and the VGPR map.  `nw` = 12 is the compact
     map of the 12-wave kernel (three waves per SIMD, at most 168 VGPRs in all):
     four operand slots read two MFMAs ahead, eight softmax temporaries, and the
-    rare path's temporaries shared with them."""
+    rare path's temporaries shared with them.  `nw` = 4 is the wide map of
+    D = 192 and 256: one wave per SIMD, O in AGPRs, K and V in two-stage LDS
+    rings of their own (rows on the 512-byte pitch)."""
 
     def __init__(self, D: int, nw: int = 8, rs: bool = False):
-        assert D in (64, 96, 128) and nw in (8, 12) and (nw == 8 or D == 64)
+        assert (D, nw) in ((64, 8), (96, 8), (128, 8), (64, 12), (192, 4), (256, 4))
         self.D = D
         self.nw = nw
+        self.wide = nw == 4
         self.rs = rs                      # row sums by MFMA: ONES (A pattern) and RS (result) tiles
-        self.nslot = NSLOT if nw == 8 else 4
-        self.NT = 16 if nw == 8 else 8       # softmax temporaries
+        self.nslot = 4 if nw == 12 else NSLOT
+        self.NT = 8 if nw == 12 else 16   # softmax temporaries
         self.NQK = D // 16                # MFMA k-steps of a score tile
         self.NDT = D // 32                # 32-wide d-tiles of O
-        # D = 96 rows sit on the D = 128 LDS pitch: chunks 12-15 of a row are
-        # filled by copy lanes reading out of range (zeros) and never read
-        self.RB = 2 * (128 if D == 96 else D)   # bytes per K/V row in LDS
+        # D = 96 rows sit on the D = 128 LDS pitch and D = 192 rows on the
+        # D = 256 pitch: the chunks past a row's data are filled by copy lanes
+        # reading out of range (zeros) and never read
+        self.RB = 2 * {96: 128, 192: 256}.get(D, D)   # bytes per K/V row in LDS
         self.TILE = 64 * self.RB          # one K or V block
-        self.VBASE = 4 * self.TILE        # V stages follow the 4 K stages
-        self.NCP = self.RB // 128         # 1 KiB copies of K (and of V) per wave and block
+        self.NST = 2 if self.wide else 4  # LDS stages per tensor
+        self.VBASE = self.NST * self.TILE  # V stages follow the K stages
+        self.NCP = self.TILE // 1024 // (4 if self.wide else 8)   # 1 KiB copies per tensor, wave and block
         r = 0
 
         def take(n: int) -> int:
             nonlocal r
             r += n
             return r - n
-        self.O = take(16 * self.NDT)
+        self.O = 0 if self.wide else take(16 * self.NDT)   # wide: a[0 : 16 NDT]
         self.Q = take(4 * self.NQK)
         self.SA, self.SB = take(16), take(16)
         self.PA, self.PB = take(8), take(8)
@@ -124,22 +130,31 @@ class Layout:
             self.LS0 = self.LS1 = self.RS        # the row sum of the sub-block: RS register 0
         else:
             self.VM, self.VL, self.LS0, self.LS1 = take(1), take(1), take(1), take(1)
-        self.DMAROW, self.C16, self.DK, self.DV = take(1), take(1), take(1), take(1)
+        # copy geometry: the row and chunk offset of a lane's copies (wide: one
+        # pair per parity of the copy index), and the lane offsets of K and V
+        npar = 2 if self.wide else 1
+        self.DMAROW = take(2 * npar)
+        self.C16 = self.DMAROW + 1
+        self.DK, self.DV = take(npar), take(npar)
         self.ROW, self.H4, self.NEGINF, self.VT = take(1), take(1), take(1), take(1)
-        if nw == 8:
-            self.RT = take(4)
-            self.T = take(16)
-        else:
+        if nw == 12:
             self.T = take(self.NT)
             self.RT = self.T                 # the rare path runs between softmaxes
+        else:
+            self.RT = take(4)
+            self.T = take(16)
         self.NVGPR = r
         sums = list(range(self.RS, self.RS + 4)) if rs else [self.LS0, self.LS1]
-        self.CLOBBER_V = (list(range(self.SA, self.KOFF)) + sums + [self.DK, self.DV] +
+        self.CLOBBER_V = (list(range(self.SA, self.KOFF)) + sums + list(range(self.DK, self.DV + npar)) +
                           list(range(min(self.RT, self.T), self.NVGPR)))
 
 
 def vr(a: int, n: int = 1) -> str:
     return f"v{a}" if n == 1 else f"v[{a}:{a + n - 1}]"
+
+
+def ar(a: int, n: int = 1) -> str:
+    return f"a{a}" if n == 1 else f"a[{a}:{a + n - 1}]"
 
 
 def sr(a: int, n: int = 1) -> str:
@@ -176,7 +191,7 @@ class Gen:
         self.mfma_order = mfma_order    # QK / PV order in a sub-iteration: alternate, in pairs, or grouped
         self.pad = pad                  # diagnostics: 16 wait states after every MFMA
         self.always_rare = always_rare  # diagnostics: exact row max on every sub-block
-        self.la = (LA if nw == 8 else 2) if la is None else la   # MFMAs of LDS operand lookahead
+        self.la = (2 if nw == 12 else LA) if la is None else la   # MFMAs of LDS operand lookahead
         assert self.la < self.L.nslot
         self.pv_b128 = pv_b128          # timing only (wrong results): one b128 read per PV operand
         self.no_softmax = no_softmax    # timing only (wrong results): no softmax VALU
@@ -197,6 +212,10 @@ class Gen:
 
     def e(self, *ins: str) -> None:
         self.lines.extend(ins)
+
+    def ov(self, a: int, n: int = 1) -> str:
+        """O registers: AGPRs in the wide map, VGPRs otherwise."""
+        return ar(a, n) if self.L.wide else vr(a, n)
 
     @property
     def mfma(self) -> str:
@@ -347,7 +366,15 @@ class Gen:
              f"v_mov_b32 {vr(L.VM)}, {vr(RT)}",
              "s_nop 0",
              f"v_mul_f32 {vr(L.VL)}, {vr(RT + 1)}, {vr(L.VL)}"]
-        r += [f"v_mul_f32 {vr(L.O + k)}, {vr(RT + 1)}, {vr(L.O + k)}" for k in range(16 * L.NDT)]
+        if L.wide:
+            # O in AGPRs: read, scale and write back through the softmax
+            # temporaries, eight at a time (free until P is recomputed below)
+            for k0 in range(0, 16 * L.NDT, 8):
+                r += [f"v_accvgpr_read_b32 {vr(L.T + i)}, {ar(L.O + k0 + i)}" for i in range(8)]
+                r += [f"v_mul_f32 {vr(L.T + i)}, {vr(RT + 1)}, {vr(L.T + i)}" for i in range(8)]
+                r += [f"v_accvgpr_write_b32 {ar(L.O + k0 + i)}, {vr(L.T + i)}" for i in range(8)]
+        else:
+            r += [f"v_mul_f32 {vr(L.O + k)}, {vr(RT + 1)}, {vr(L.O + k)}" for k in range(16 * L.NDT)]
         r += self.softmax_ops(S, P)
         if self.rs_mfma:
             r += ["s_nop 7", "s_nop 3", f"s_setpc_b64 {sr(S_RET, 2)}"]
@@ -423,6 +450,49 @@ class Gen:
             r.append(f"s_add_u32 {sr(S_SOV + 1)}, {sr(S_SOV)}, {sr(S_KRSC + 3)}")
         return r
 
+    def decode_wide(self, x: int, site: str, v: bool) -> list[str]:
+        """Wide map: soffsets of the K (or V) copies of the block named by entry
+        word x, copy ii taking rows 16*(ii >> 1) on (four soffsets).  K and V of
+        one iteration belong to different blocks, so each tensor tracks its own
+        key source (SWITCHK / SWITCHV)."""
+        t = "V" if v else "K"
+        cur, so, stride, st16 = (S_CURV, S_SOVW, S_KRSC + 1, S_KRSC + 3) if v else (S_CUR, S_SOK, S_KRSC, S_KRSC + 2)
+        self.stubs += [f"{lbl(f'SWSTUB{t}_' + site)}:", f"s_call_b64 {sr(S_RET, 2)}, {lbl('SWITCH' + t)}",
+                       f"s_branch {lbl(f'SWRET{t}_' + site)}"]
+        r = [f"s_lshr_b32 s74, {sr(x)}, 31", f"s_cmp_lg_u32 s74, {sr(cur)}",
+             f"s_cbranch_scc1 {lbl(f'SWSTUB{t}_' + site)}",
+             f"{lbl(f'SWRET{t}_' + site)}:",
+             f"s_and_b32 s73, {sr(x)}, 0x7fffffff",
+             "s_lshl_b32 s73, s73, 6",                                  # first row of the block
+             f"s_mul_i32 {sr(so)}, s73, {sr(stride)}"]
+        r += [f"s_add_u32 {sr(so + i)}, {sr(so + i - 1)}, {sr(st16)}" for i in range(1, 4)]   # + 16 rows
+        return r
+
+    def switch_wide(self, v: bool) -> list[str]:
+        """Wide map: buffer resource, row stride, 16-row stride and the lane copy
+        offsets (both parities) of K (or V) for key source s74."""
+        L = self.L
+        t = "V" if v else "K"
+        cur, rs, st, st16, kb, off = ((S_CURV, S_RV, S_KRSC + 1, S_KRSC + 3, (S_VB0, S_VB1), L.DV) if v else
+                                      (S_CUR, S_RK, S_KRSC, S_KRSC + 2, (S_KB0, S_KB1), L.DK))
+        srs = (S_VRS0, S_VRS1) if v else (S_KRS0, S_KRS1)
+        return [
+            f"{lbl('SWITCH' + t)}:",
+            f"s_mov_b32 {sr(cur)}, s74",
+            "s_cmp_eq_u32 s74, 0",
+            f"s_cselect_b32 s75, {sr(S_NK)}, {sr(S_NX)}",
+            f"s_cselect_b32 {sr(st)}, {sr(srs[0])}, {sr(srs[1])}",
+            f"s_cselect_b64 {sr(rs, 2)}, {sr(kb[0], 2)}, {sr(kb[1], 2)}",
+            f"s_and_b32 {sr(rs + 1)}, {sr(rs + 1)}, 0xffff",
+            f"s_mul_i32 {sr(rs + 2)}, s75, {sr(st)}",
+            f"s_mov_b32 {sr(rs + 3)}, 0x20000",
+            f"s_lshl_b32 {sr(st16)}, {sr(st)}, 4",
+            f"v_mad_u32_u24 {vr(off)}, {vr(L.DMAROW)}, {sr(st)}, {vr(L.C16)}",
+            f"v_mad_u32_u24 {vr(off + 1)}, {vr(L.DMAROW + 2)}, {sr(st)}, {vr(L.C16 + 2)}",
+            "s_nop 1",
+            f"s_setpc_b64 {sr(S_RET, 2)}",
+        ]
+
     def switch_routine(self) -> list[str]:
         """Buffer resources, row strides and lane copy offsets of key source s74."""
         L = self.L
@@ -455,11 +525,20 @@ class Gen:
         rows 32*ii + 4*wave + lane/16 (D = 128) or 8*wave + lane/8 (D = 64)."""
         L = self.L
         v, ii = k // L.NCP, k % L.NCP
-        lds = (L.VBASE if v else 0) + stage * L.TILE + ii * 8192
         rs = S_RV if v else S_RK
-        so = sr((S_SOV if v else S_SOK) + ii)
+        if L.wide:
+            # copy ii of wave w fills LDS KiB 4*ii + w of the block: rows
+            # 8*ii + 2*w + lane/32; rows 16*(ii >> 1) in the soffset, the rest
+            # (and the swizzle, which depends on ii's parity) in the lane offset
+            lds = (L.VBASE if v else 0) + stage * L.TILE + ii * 4096
+            so = sr((S_SOVW if v else S_SOK) + (ii >> 1))
+            lane = (L.DV if v else L.DK) + (ii & 1)
+        else:
+            lds = (L.VBASE if v else 0) + stage * L.TILE + ii * 8192
+            so = sr((S_SOV if v else S_SOK) + ii)
+            lane = L.DV if v else L.DK
         return [f"s_add_u32 m0, {sr(S_LDSK)}, {lds}", "s_nop 0",
-                f"buffer_load_dwordx4 {vr(L.DV if v else L.DK)}, {sr(rs, 4)}, {so} offen lds"]
+                f"buffer_load_dwordx4 {vr(lane)}, {sr(rs, 4)}, {so} offen lds"]
 
     def place_copy(self, fill: dict[int, list[str]], at: int, stage: int, k: int) -> None:
         """Copy k of a block after MFMA `at`; with copy_split, its M0 is set after
@@ -525,7 +604,7 @@ class Gen:
                     self.e(f"{self.mfma} {vr(S, 16)}, {vr(slot, 4)}, {vr(L.Q + 4 * c, 4)}, {vr(S, 16)}")
             else:
                 _, _, st16, dt, P = m
-                acc = vr(L.O + 16 * dt, 16)
+                acc = self.ov(L.O + 16 * dt, 16)
                 self.e(f"{self.mfma} {acc}, {vr(slot, 4)}, {vr(P + 4 * (st16 & 1), 4)}, {acc}")
             if self.pad:
                 self.e("s_nop 15")
@@ -567,16 +646,18 @@ class Gen:
         """Block j: QK of its two sub-blocks (K in `stage`), softmax of sub-blocks
         2j-1 and 2j, PV of block j-1 (V in stage-1), copies of block j+2."""
         L = self.L
-        vst, cst = (stage + 3) & 3, (stage + 2) & 3
+        vst, cst = (stage + 3) & 3, (stage + 2) & 3       # entry slots of blocks j-1 and j+2
+        # LDS stages of K(j) and V(j-1) (wide: two-stage rings of their own)
+        kld, vld = (stage & 1, (stage + 1) & 1) if L.wide else (stage, vst)
         site = f"I{stage}"
         M = 2 * L.NQK                     # MFMAs per sub-iteration (QK and PV interleaved)
-        self.e(f"; ── block j, K stage {stage}", f"s_waitcnt vmcnt({2 * L.NCP})",
+        self.e(f"; ── block j, K stage {stage}", f"s_waitcnt vmcnt({0 if L.wide else 2 * L.NCP})",
                "s_nop 0" if self.no_barrier else "s_barrier", "s_waitcnt lgkmcnt(0)")
         mf = []
         half_q = L.NQK // 2               # QK k-steps per 16-key PV step
         for half, S, P in ((0, L.SA, L.PA), (1, L.SB, L.PB)):
-            qks = [("qk", stage, half, c, S) for c in range(L.NQK)]
-            pvs = [("pv", vst, 2 * half + c // half_q, c % L.NDT, P) for c in range(L.NQK)]
+            qks = [("qk", kld, half, c, S) for c in range(L.NQK)]
+            pvs = [("pv", vld, 2 * half + c // half_q, c % L.NDT, P) for c in range(L.NQK)]
             lead = len(self.lead_pv(vst)) if half == 0 else 0
             mf += pvs[:lead]
             rest = pvs[lead:]
@@ -588,11 +669,18 @@ class Gen:
                 mf += qks[c:c + step] + rest[c:c + step]
             mf += rest[L.NQK:]
         assert mf[:len(self.lead_pv(vst))] == self.lead_pv(vst)
-        fill: dict[int, list[str]] = {0: [] if self.no_decode else self.decode(S_ENT + 2 * cst, site)}
-        # copies after MFMAs spread over the block's 4*NQK MFMAs
-        at_copy = {8: (6, 10, 22, 26), 6: (4, 8, 16, 20), 4: (5, 13)}[L.NQK]
-        for k, at in enumerate(at_copy):
-            self.place_copy(fill, at, cst, k)
+        if L.wide:
+            # K(j+1) into the K stage K(j-1) left, V(j) into the V stage V(j-2) left
+            fill = {0: [] if self.no_decode else (self.decode_wide(S_ENT + 2 * ((stage + 1) & 3), site, False) +
+                                                  self.decode_wide(S_ENT + 2 * stage, site, True))}
+            for k in range(2 * L.NCP):
+                self.place_copy(fill, 1 + 2 * k, (stage + 1) & 1 if k < L.NCP else stage & 1, k)
+        else:
+            fill = {0: [] if self.no_decode else self.decode(S_ENT + 2 * cst, site)}
+            # copies after MFMAs spread over the block's 4*NQK MFMAs
+            at_copy = {8: (6, 10, 22, 26), 6: (4, 8, 16, 20), 4: (5, 13)}[L.NQK]
+            for k, at in enumerate(at_copy):
+                self.place_copy(fill, at, cst, k)
         sm = self.sm_start
         # sub-iteration a: softmax of sub-block 2j-1 (S_B, block j-1 half 1)
         fill.setdefault(sm - 1, []).extend(self.mask_check(site + "a", "B", S_ENT + 2 * vst + 1, 1))
@@ -609,11 +697,18 @@ class Gen:
     def first_iteration(self) -> None:
         """Block 0: QK of its two sub-blocks, softmax of sub-block 0, copies of block 2."""
         L = self.L
-        self.e("; ── block 0", f"s_waitcnt vmcnt({2 * L.NCP})", "s_barrier", "s_waitcnt lgkmcnt(0)")
+        self.e("; ── block 0", f"s_waitcnt vmcnt({0 if L.wide else 2 * L.NCP})", "s_barrier", "s_waitcnt lgkmcnt(0)")
         mf = [("qk", 0, 0, c, L.SA) for c in range(L.NQK)] + [("qk", 0, 1, c, L.SB) for c in range(L.NQK)]
-        fill: dict[int, list[str]] = {0: self.decode(S_ENT + 4, "F")}
-        for k in range(2 * L.NCP):
-            self.place_copy(fill, 1 + k, 2, k)
+        if L.wide:
+            # K(1) into K stage 1, V(0) into V stage 0, spread over the block's QK MFMAs
+            fill = {0: self.decode_wide(S_ENT + 2, "F", False) + self.decode_wide(S_ENT, "F", True)}
+            n = len(mf)
+            for k in range(2 * L.NCP):
+                self.place_copy(fill, 1 + (k * (n - 2)) // (2 * L.NCP - 1), 1 if k < L.NCP else 0, k)
+        else:
+            fill = {0: self.decode(S_ENT + 4, "F")}
+            for k in range(2 * L.NCP):
+                self.place_copy(fill, 1 + k, 2, k)
         fill.setdefault(L.NQK + 1, []).extend(self.mask_check("F", "A", S_ENT + 1, 0))
         self.place_softmax(fill, L.SA, L.PA, list(range(L.NQK + 2, 2 * L.NQK - 1)), 2 * L.NQK - 1, "F", "A")
         self.stream(mf, fill, nxt=self.lead_pv(0))
@@ -623,9 +718,13 @@ class Gen:
         """After block n-1 (in `stage`): softmax of sub-block 2n-1, PV of block n-1."""
         L = self.L
         self.e(f"{lbl(f'DRAIN{stage}')}:")
+        vld = stage & 1 if L.wide else stage
+        if L.wide:
+            # V(n-1) was copied during block n-1: wait for every wave's copies
+            self.e("s_waitcnt vmcnt(0)", "s_barrier")
         nh = L.NQK                        # PV MFMAs per half: 2 16-key steps x NDT d-tiles
-        mf = [("pv", stage, k // L.NDT, k % L.NDT, L.PA) for k in range(nh)] + \
-             [("pv", stage, 2 + k // L.NDT, k % L.NDT, L.PB) for k in range(nh)]
+        mf = [("pv", vld, k // L.NDT, k % L.NDT, L.PA) for k in range(nh)] + \
+             [("pv", vld, 2 + k // L.NDT, k % L.NDT, L.PB) for k in range(nh)]
         fill: dict[int, list[str]] = {0: self.mask_check(f"D{stage}", "B", S_ENT + 2 * stage + 1, 1)}
         self.place_softmax(fill, L.SB, L.PB, list(range(1, nh - 1)), nh - 1, f"D{stage}", "B")
         self.stream(mf, fill)
@@ -647,10 +746,17 @@ class Gen:
           f"s_mov_b32 {sr(S_J)}, 0",
           f"s_mov_b32 {sr(S_CUR)}, 2",
           "s_waitcnt lgkmcnt(0)")
-        for blk in (0, 1):
-            e(*self.decode(S_ENT + 2 * blk, f"S{blk}"))
-            for k in range(2 * L.NCP):
-                e(*self.copy(blk, k))
+        if L.wide:
+            # K(0) into K stage 0; V(0) and K(1) follow in block 0
+            e(f"s_mov_b32 {sr(S_CURV)}, 2")
+            e(*self.decode_wide(S_ENT, "S0", False))
+            for k in range(L.NCP):
+                e(*self.copy(0, k))
+        else:
+            for blk in (0, 1):
+                e(*self.decode(S_ENT + 2 * blk, f"S{blk}"))
+                for k in range(2 * L.NCP):
+                    e(*self.copy(blk, k))
         self.first_iteration()
         e(f"{lbl('LOOP')}:")
         for stage in (1, 2, 3, 0):
@@ -661,8 +767,8 @@ class Gen:
             self.phase = loop_phase
             self.drain(stage)
         e(*self.stubs)
-        e(*self.rare_routine(L.SA, L.PA, "RARE_A"), *self.rare_routine(L.SB, L.PB, "RARE_B"),
-          *self.switch_routine())
+        e(*self.rare_routine(L.SA, L.PA, "RARE_A"), *self.rare_routine(L.SB, L.PB, "RARE_B"))
+        e(*(self.switch_wide(False) + self.switch_wide(True) if L.wide else self.switch_routine()))
         e(*self.mask_routine(L.SA, "MASK_A"), *self.mask_routine(L.SB, "MASK_B"))
         e(f"{lbl('END')}:")
         return self.lines
@@ -677,14 +783,16 @@ def operands(D: int, nw: int = 8, rs: bool = False) -> list[str]:
     L = Layout(D, nw, rs)
     pf = prefix(D, nw)
     os_ = ", ".join(f"o{t}" for t in range(L.NDT))
-    outs = ", ".join(f'"+{{{vr(L.O + 16 * t, 16)}}}"(o{t})' for t in range(L.NDT))
+    orr = ar if L.wide else vr          # the wide map keeps O in AGPRs
+    outs = ", ".join(f'"+{{{orr(L.O + 16 * t, 16)}}}"(o{t})' for t in range(L.NDT))
     outs += f', "+{{{vr(L.VM, 2)}}}"(ml), "+{{{vr(L.ROW, 4)}}}"(misc)'
-    if 4 * L.NQK == 24:   # no 24-register operand class: Q as 16 + 8 registers (qv.lo, qv.hi)
-        q = f'"{{{vr(L.Q, 16)}}}"(qv.lo), "{{{vr(L.Q + 16, 8)}}}"(qv.hi)'
+    if 4 * L.NQK in (24, 48, 64):   # no such operand class (or too wide): Q as two operands (qv.lo, qv.hi)
+        lo = 16 if 4 * L.NQK == 24 else 32
+        q = f'"{{{vr(L.Q, lo)}}}"(qv.lo), "{{{vr(L.Q + lo, 4 * L.NQK - lo)}}}"(qv.hi)'
     else:
         q = f'"{{{vr(L.Q, 4 * L.NQK)}}}"(qv)'
     ins = (f'{q}, "{{{vr(L.KOFF, L.NQK)}}}"(koff), '
-           f'"{{{vr(L.VOFFA, 2 * L.NDT)}}}"(voff), "{{{vr(L.DMAROW, 2)}}}"(dma), '
+           f'"{{{vr(L.VOFFA, 2 * L.NDT)}}}"(voff), "{{{vr(L.DMAROW, 4 if L.wide else 2)}}}"(dma), '
            f'"{{s[20:23]}}"(sa), "{{s[24:31]}}"(sb), "{{s[32:39]}}"(sc)')
     if L.rs:
         ins += f', "{{{vr(L.ONES, 4)}}}"(ones)'
@@ -718,7 +826,11 @@ PRODUCT = {128: dict(lead=2, early_load=True, dot_init=True, and_scc=True, copy_
                      tail_split=True, mask_fast=True),
            96: dict(lead=2, early_load=True, dot_init=True, and_scc=True, copy_split=True, rs_mfma=True,
                     tail_split=True, mask_fast=True),
-           64: dict(dot_init=True, and_scc=True, copy_split=True, rs_mfma=True, tail_split=True, mask_fast=True)}
+           64: dict(dot_init=True, and_scc=True, copy_split=True, rs_mfma=True, tail_split=True, mask_fast=True),
+           256: dict(early_load=True, dot_init=True, and_scc=True, copy_split=True, rs_mfma=True, tail_split=True,
+                     mask_fast=True),
+           192: dict(early_load=True, dot_init=True, and_scc=True, copy_split=True, rs_mfma=True, tail_split=True,
+                     mask_fast=True)}
 
 
 def render(per_d: dict | None = None, **opts) -> str:
@@ -726,7 +838,7 @@ def render(per_d: dict | None = None, **opts) -> str:
            "// attn_fwd_stream_kernel (lvsa_attn_stream.h) and their asm operand lists.",
            "// Do not edit; regenerate.",
            "#pragma once", ""]
-    for D, nw in ((128, 8), (96, 8), (64, 8), (64, 12)):
+    for D, nw in ((128, 8), (96, 8), (64, 8), (64, 12), (256, 4), (192, 4)):
         pf = prefix(D, nw)
         for dt, name in (("bf16", f"{pf}_LOOP_BF16"), ("f16", f"{pf}_LOOP_F16")):
             o = {**PRODUCT[D], **opts, **(per_d or {}).get(D, {})}

@@ -272,12 +272,18 @@ extern "C" int lvsa_attn_fwd(const lvsa_attn_args* a, hipStream_t stream) {
   // 32-bit byte offsets; at D = 96 the lanes of the unused chunks of a row add
   // 0x7FFF0000 to theirs (out of range: zeros, no access), so the rows must
   // stay below 2^31 bytes there.
-  const int64_t lim = a->D == 96 ? (1LL << 31) : (1LL << 32);
+  const int64_t lim = (a->D == 96 || a->D == 192) ? (1LL << 31) : (1LL << 32);
   auto fits32 = [lim](int64_t rows, int64_t row_elems) { return (rows + kBN) * row_elems * 2 < lim; };
   const bool src32 = fits32(a->n_k, a->k_str[1]) && fits32(a->n_k, a->v_str[1]) &&
                      (a->n_x == 0 || (fits32(a->n_x, a->kx_str[1]) && fits32(a->n_x, a->vx_str[1])));
   p.use_stream = (!fp32 && (a->D == 128 || a->D == 96 || a->D == 64) && a->block_q == kPPBM && !force_pp && src32 &&
                   (a->n_q == 0 || (p.R >= 255 && p.C >= 64))) ? 1 : 0;
+  // D = 192 and 256: the wide single-stream loop on the 4-wave kernel's
+  // 128-row tiles, which touch at most two query frames when frames have
+  // >= 127 rows.
+  if (!fp32 && (a->D == 192 || a->D == 256) && a->block_q == kBM && !force_pp && src32 &&
+      (a->n_q == 0 || (p.R >= 127 && p.C >= 64)))
+    p.use_stream = 1;
   if (a->block_q == kStream12BM) {
     LVSA_REQUIRE(src32, LVSA_ERR_UNSUPPORTED,
                  "lvsa_attn_fwd: 384-row tiles address each key source with 32-bit byte offsets (source too large)");

@@ -105,7 +105,7 @@ class Wave:
     def __init__(self, wid, sim):
         self.w = wid
         self.sim = sim
-        self.v = np.zeros((256, 64), dtype=np.uint32)
+        self.v = np.zeros((512, 64), dtype=np.uint32)   # VGPRs, then AGPRs a0.. at 256..
         self.s = [0] * 112
         self.vcc = 0
         self.scc = 0
@@ -115,11 +115,12 @@ class Wave:
 
     # operand helpers
     def vreg(self, tok):
-        m = re.fullmatch(r'v(\d+)', tok)
+        base = 256 if tok[0] == 'a' else 0          # AGPRs follow the VGPRs
+        m = re.fullmatch(r'[va](\d+)', tok)
         if m:
-            return int(m.group(1)), 1
-        m = re.fullmatch(r'v\[(\d+):(\d+)\]', tok)
-        return int(m.group(1)), int(m.group(2)) - int(m.group(1)) + 1
+            return base + int(m.group(1)), 1
+        m = re.fullmatch(r'[va]\[(\d+):(\d+)\]', tok)
+        return base + int(m.group(1)), int(m.group(2)) - int(m.group(1)) + 1
 
     def sreg(self, tok):
         m = re.fullmatch(r's(\d+)', tok)
@@ -166,7 +167,7 @@ class Wave:
         neg = tok.startswith('-')
         if neg:
             tok = tok[1:]
-        if tok.startswith('v'):
+        if tok.startswith(('v', 'a')):
             x = self.v[self.vreg(tok)[0]].copy()
         elif tok.startswith('s'):
             x = np.full(64, self.s[self.sreg(tok)[0]], dtype=np.uint32)
@@ -422,7 +423,7 @@ class Wave:
             a0, a1 = pairs(self.vsrc_u(a[1]))
             b0, b1 = pairs(self.vsrc_u(a[2]))
             self.vdst(a[0], (a0 * b0 + a1 * b1 + self.vsrc_f(a[3])).astype(np.float32))
-        elif op == 'v_mov_b32':
+        elif op in ('v_mov_b32', 'v_accvgpr_read_b32', 'v_accvgpr_write_b32'):
             self.vdst(a[0], self.vsrc_u(a[1]))
         elif op == 'v_add_f32':
             self.vdst(a[0], (self.vsrc_f(a[1]) + self.vsrc_f(a[2])).astype(np.float32))

@@ -686,12 +686,13 @@ def _stream_cfg(seed):
     return T, P, W, n, kfi, off, H, Hkv, n_txt, dt
 
 
-@pytest.mark.parametrize("D", [128, 64, 96])
+@pytest.mark.parametrize("D", [128, 64, 96, 192, 256])
 @pytest.mark.parametrize("seed", range(16))
 def test_stream_kernel_random_geometries(seed, D, gpu, monkeypatch):
-    """D = 64, 96 and 128 on frames of >= 255 tokens run the hand-scheduled
-    single-stream kernel; against the fp32 oracle, and the ping-pong kernel
-    within bf16 rounding."""
+    """D = 64, 96 and 128 on frames of >= 255 tokens, and D = 192 and 256 (the
+    wide map, 128-row tiles) on frames of >= 127, run the hand-scheduled
+    single-stream kernel; against the fp32 oracle, and the ping-pong (D >= 192:
+    4-wave) kernel within bf16 rounding."""
     T, P, W, n, kfi, off, H, Hkv, n_txt, dt = _stream_cfg(seed)
     N = T * P
     m = _meta(T, P, W, n, kfi, off)

@@ -26,8 +26,9 @@ def test_committed_loop_is_generated():
 
 def _swz(r, D=128):
     """16-byte chunk swizzle of LDS row r (lvsa_attn_kernels.h swz<D>; D = 96
-    rows use the D = 128 layout)."""
-    if D in (96, 128):
+    rows use the D = 128 layout, D = 192 and 256 the D = 128 swizzle on the
+    low four chunk bits)."""
+    if D in (96, 128, 192, 256):
         return ((r & 3) << 2) | ((r >> 2) & 3)
     return (((r >> 1) & 1) << 2) | (((r >> 2) & 1) << 1) | ((r >> 3) & 1)
 
@@ -88,11 +89,21 @@ def run_loop(entries, nk, n_x, seed=0, dt="bf16", D=128, nw=8, **opts):
             V[L.VOFFA + dt_] = L.VBASE + rowA * RB + ((chunk ^ np.array([_swz(x, D) for x in rowA])) << 4) + inb
             V[L.VOFFB + dt_] = (L.VBASE + (rowA + 8) * RB +
                                 ((chunk ^ np.array([_swz(x, D) for x in rowA + 8])) << 4) + inb)
-        crow = (w % 8) * (1024 // RB) + lane // NCH
-        V[L.DMAROW] = crow
-        V[L.C16] = ((lane % NCH) ^ np.array([_swz(x & 15, D) for x in crow])) * 16
-        if D == 96:   # chunks past the row's data: an offset beyond every source (zeros, no access)
-            V[L.C16] = np.where(V[L.C16] >= 16 * 12, 0x7FFF0000, V[L.C16])
+        ndata = 2 * D // 16                   # chunks of a row that hold data
+        if L.wide:
+            # copy ii fills LDS KiB 4*ii + w: rows 8*ii + 2*w + lane/32, one
+            # (row, chunk offset) pair per parity of ii
+            for par in (0, 1):
+                crow = 8 * par + 2 * w + lane // 32
+                c16 = ((lane % NCH) ^ np.array([_swz(x & 15, D) for x in crow])) * 16
+                V[L.DMAROW + 2 * par] = crow
+                V[L.C16 + 2 * par] = np.where(c16 >= 16 * ndata, 0x7FFF0000, c16)
+        else:
+            crow = (w % 8) * (1024 // RB) + lane // NCH
+            V[L.DMAROW] = crow
+            V[L.C16] = ((lane % NCH) ^ np.array([_swz(x & 15, D) for x in crow])) * 16
+            if ndata < NCH:   # chunks past the row's data: an offset beyond every source (zeros, no access)
+                V[L.C16] = np.where(V[L.C16] >= 16 * ndata, 0x7FFF0000, V[L.C16])
         V[L.ROW], V[L.H4], V[L.NEGINF], V[L.VT] = 32 * w + i32, 4 * h, 0xFF800000, 0
         V[L.VM] = A.f2u(np.full(64, -1e30, np.float32))
         if L.rs:
@@ -110,12 +121,13 @@ def run_loop(entries, nk, n_x, seed=0, dt="bf16", D=128, nw=8, **opts):
     sim.run(waves)
     O = np.zeros((R, D))
     lsum, mrun = np.zeros(R), np.zeros(R)
+    obase = 256 if L.wide else 0          # the wide map keeps O in AGPRs
     for w, W in enumerate(waves):
         for ln in range(64):
             r, hh = 32 * w + (ln & 31), ln >> 5
             for dt_ in range(L.NDT):
                 for rr in range(16):
-                    O[r, 32 * dt_ + 8 * (rr // 4) + 4 * hh + rr % 4] = A.u2f(W.v[L.O + 16 * dt_ + rr, ln])
+                    O[r, 32 * dt_ + 8 * (rr // 4) + 4 * hh + rr % 4] = A.u2f(W.v[obase + L.O + 16 * dt_ + rr, ln])
             lsum[r] += A.u2f(W.v[L.VL, ln])
             mrun[r] = A.u2f(W.v[L.VM, ln])
     # reference: float64 softmax attention over the allowed keys
@@ -200,3 +212,32 @@ def test_loop_rare_path_every_sub_block(D):
 def test_loop_fp16(D):
     err, lse_err, _ = run_loop([(j, _tail(150, j)) for j in range(3)], 150, 0, seed=4, dt="f16", D=D)
     assert err <= 2e-3 and lse_err <= 2e-3
+
+
+@pytest.mark.parametrize("D", [256, 192])
+@pytest.mark.parametrize("case", sorted(CASES))
+def test_wide_loop(case, D):
+    """The wide map of D = 192 and 256: 4 waves (one per SIMD) on 128 query
+    rows, O in AGPRs, K and V in two-stage rings of their own (K of block
+    j + 1 and V of block j copied during block j); rows on the 512-byte
+    pitch (D = 192: chunks 24-31 zero-filled and never read)."""
+    make, nk, n_x = CASES[case]
+    entries = make()
+    err, lse_err, copies = run_loop(entries, nk, n_x, D=D, nw=4)
+    assert err <= 4e-3 and lse_err <= 2e-3, (case, err, lse_err)
+    # K(0) in the setup, then K(j + 1) and V(j) in every block: 8 copies per tensor
+    assert copies == 4 * 8 * (1 + 2 * len(entries))
+
+
+@pytest.mark.parametrize("D", [256, 192])
+def test_wide_loop_source_switches_rare_path_and_fp16(D):
+    """K and V of one block come from different plan entries: sources switch
+    (video -> extra rows -> video) for each tensor on its own; the exact-max
+    path on every sub-block; fp16."""
+    ent = [(0, 0), (0x80000000, _tail(5, 0)), (1, 0), (2, _tail(150, 2))]
+    err, lse_err, _ = run_loop(ent, 150, 5, seed=8, D=D, nw=4)
+    assert err <= 4e-3 and lse_err <= 2e-3, (err, lse_err)
+    err, lse_err, _ = run_loop([(j, 0) for j in range(3)], 192, 0, seed=3, D=D, nw=4, always_rare=True)
+    assert err <= 4e-3 and lse_err <= 2e-3, (err, lse_err)
+    err, lse_err, _ = run_loop([(j, _tail(150, j)) for j in range(3)], 150, 0, seed=4, dt="f16", D=D, nw=4)
+    assert err <= 2e-3 and lse_err <= 2e-3, (err, lse_err)
