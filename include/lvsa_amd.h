@@ -220,7 +220,7 @@ typedef struct lvsa_attn_args {
    *   launch (exact log-sum-exp merge, as flashinfer_runner.py:184-197), so
    *   the long text tiles fill the launch's last round instead of
    *   lengthening it;
-   * - the single-stream kernel (D = 64, 96 and 128) runs one persistent
+   * - the single-stream kernel (every 16-bit head size) runs one persistent
    *   work-group per CU that takes work items from eight per-XCD queues
    *   (counters in the last 1 KiB, zeroed by the call) and steals from the
    *   other XCDs' queues once its own is empty, so XCDs that run faster take

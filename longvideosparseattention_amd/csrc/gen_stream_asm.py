@@ -1,4 +1,4 @@
-"""Generate the key loop of the single-stream attention kernel (D = 64, 96 and 128).
+"""Generate the key loop of the single-stream attention kernel (every 16-bit head size).
 
     python gen_stream_asm.py [out.inc]   (default: lvsa_attn_stream_body.inc beside this file)
 
@@ -59,6 +59,12 @@ Register map (VGPRs; the kernel's operands pin them), D = 128 (D = 64):
   D = 96 (6 k-steps, 3 d-tiles) follows the D = 128 map with fewer O, Q and
   offset registers (202 VGPRs) and uses the D = 128 LDS layout: 256-byte rows
   whose chunks 12-15 the copies fill with zeros and no read touches.
+  D = 192 and 256 use the wide map (Layout nw = 4): 4 waves of 32 rows, one per
+  SIMD, O in AGPRs a[0 : 16 NDT], Q from v0, two lane copy offsets per tensor
+  (the swizzle of copy ii depends on its parity) and four soffsets; 512-byte
+  rows, K and V in two-stage rings of their own: block j copies K(j+1) and V(j)
+  and waits for all copies at the next barrier, K and V tracking their key
+  sources separately (SWITCHK / SWITCHV).  218 (194) VGPRs.
 SGPRs: s[20:21] entry pointer, s22 blocks, s23 scale*log2(e), s[24:31] K/V
 bases (video, extra), s32-35 row strides, s36-37 source lengths, s38 wave,
 s39 LDS copy base of the wave; s40-s95 scratch.

@@ -261,7 +261,7 @@ extern "C" int lvsa_attn_fwd(const lvsa_attn_args* a, hipStream_t stream) {
   p.text_chunks = chunks;
   p.text_first = chunks == 1 ? 1 : 0;
   p.ws = chunks > 1 ? (float*)a->workspace : nullptr;
-  // The single-stream kernel (D = 64, 96 and 128) serves plans without generic descriptors:
+  // The single-stream kernel (D = 64, 96 and 128 here) serves plans without generic descriptors:
   // 256-row tiles touch at most two query frames when frames have >= 255
   // rows, and 64-key blocks (even short last ones) at most two key frames
   // when frames have >= 64 keys.  LVSA_ATTN_KERNEL=pp selects the ping-pong
