@@ -823,7 +823,10 @@ def operands(D: int, nw: int = 8, rs: bool = False) -> list[str]:
 # and an add per sub-block (Wan 4x 2.7%, CogVideoX 1.9%), issue the rare
 # test one MFMA before its branch (Wan 4x 1.2%, CogVideoX 0.6%), and mask a
 # sub-block that lies on one side of the key split with one lane mask
-# (CogVideoX 1.0%, Wan 4x 0.25%).  Measured
+# (CogVideoX 1.0%, Wan 4x 0.25%).  The wide map (D = 192, 256) reads operands
+# four MFMAs ahead and starts each softmax four MFMA slots into its
+# sub-iteration (1.2% / 1.4% faster than 3 and 2; lookahead 2 and 5, start 3
+# and no mid-block entry load measured slower).  Measured
 # neutral and not used: the D = 64 softmax spread over one more MFMA slot
 # (sm_start 1), one LDS wait per two MFMAs (wait_pair), 8 wait states before
 # the row sum is read (tail_nop 8), QK / PV MFMAs in pairs or grouped
@@ -834,9 +837,9 @@ PRODUCT = {128: dict(lead=2, early_load=True, dot_init=True, and_scc=True, copy_
                     tail_split=True, mask_fast=True),
            64: dict(dot_init=True, and_scc=True, copy_split=True, rs_mfma=True, tail_split=True, mask_fast=True),
            256: dict(early_load=True, dot_init=True, and_scc=True, copy_split=True, rs_mfma=True, tail_split=True,
-                     mask_fast=True),
+                     mask_fast=True, la=4, sm_start=4),
            192: dict(early_load=True, dot_init=True, and_scc=True, copy_split=True, rs_mfma=True, tail_split=True,
-                     mask_fast=True)}
+                     mask_fast=True, la=4, sm_start=4)}
 
 
 def render(per_d: dict | None = None, **opts) -> str:
