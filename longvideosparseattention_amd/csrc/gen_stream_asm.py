@@ -180,7 +180,7 @@ class Gen:
                  and_scc: bool = False, copy_split: bool = False, sm_start: int = 2, rs_mfma: bool = False,
                  wait_pair: bool = False, rs_mix: bool = False, tail_nop: int = 12, no_switch: bool = False,
                  no_fma: bool = False, qk_dup: bool = False, no_rare: bool = False, tail_split: bool = False,
-                 mask_fast: bool = False, mfma_order: str = "alt"):
+                 mask_fast: bool = False, mfma_order: str = "alt", copy_every: int = 2):
         assert dt in ("bf16", "f16")
         self.dt = dt
         self.L = Layout(D, nw, rs=rs_mfma)
@@ -195,6 +195,7 @@ class Gen:
         self.tail_split = tail_split    # rare test issued one MFMA before its branch
         self.mask_fast = mask_fast      # MASK: one lane mask for all 16 keys when the key split lies outside
         self.mfma_order = mfma_order    # QK / PV order in a sub-iteration: alternate, in pairs, or grouped
+        self.copy_every = copy_every    # wide map: MFMAs between a block's copies
         self.pad = pad                  # diagnostics: 16 wait states after every MFMA
         self.always_rare = always_rare  # diagnostics: exact row max on every sub-block
         self.la = (2 if nw == 12 else LA) if la is None else la   # MFMAs of LDS operand lookahead
@@ -680,7 +681,7 @@ class Gen:
             fill = {0: [] if self.no_decode else (self.decode_wide(S_ENT + 2 * ((stage + 1) & 3), site, False) +
                                                   self.decode_wide(S_ENT + 2 * stage, site, True))}
             for k in range(2 * L.NCP):
-                self.place_copy(fill, 1 + 2 * k, (stage + 1) & 1 if k < L.NCP else stage & 1, k)
+                self.place_copy(fill, 1 + self.copy_every * k, (stage + 1) & 1 if k < L.NCP else stage & 1, k)
         else:
             fill = {0: [] if self.no_decode else self.decode(S_ENT + 2 * cst, site)}
             # copies after MFMAs spread over the block's 4*NQK MFMAs
@@ -826,7 +827,9 @@ def operands(D: int, nw: int = 8, rs: bool = False) -> list[str]:
 # (CogVideoX 1.0%, Wan 4x 0.25%).  The wide map (D = 192, 256) reads operands
 # four MFMAs ahead and starts each softmax four MFMA slots into its
 # sub-iteration (1.2% / 1.4% faster than 3 and 2; lookahead 2 and 5, start 3
-# and no mid-block entry load measured slower).  Measured
+# and no mid-block entry load measured slower); at D = 256 its copies go out
+# every third MFMA (1.0% faster than every second; at D = 192, whose blocks
+# have 48 MFMAs, 8% slower; every MFMA 3-5% slower).  Measured
 # neutral and not used: the D = 64 softmax spread over one more MFMA slot
 # (sm_start 1), one LDS wait per two MFMAs (wait_pair), 8 wait states before
 # the row sum is read (tail_nop 8), QK / PV MFMAs in pairs or grouped
@@ -837,7 +840,7 @@ PRODUCT = {128: dict(lead=2, early_load=True, dot_init=True, and_scc=True, copy_
                     tail_split=True, mask_fast=True),
            64: dict(dot_init=True, and_scc=True, copy_split=True, rs_mfma=True, tail_split=True, mask_fast=True),
            256: dict(early_load=True, dot_init=True, and_scc=True, copy_split=True, rs_mfma=True, tail_split=True,
-                     mask_fast=True, la=4, sm_start=4),
+                     mask_fast=True, la=4, sm_start=4, copy_every=3),
            192: dict(early_load=True, dot_init=True, and_scc=True, copy_split=True, rs_mfma=True, tail_split=True,
                      mask_fast=True, la=4, sm_start=4)}
 
