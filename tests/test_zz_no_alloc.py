@@ -37,7 +37,7 @@ def _noalloc(gpu, m, q, k, v, qt, kt, vt):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("D", [128, 64, 96])
+@pytest.mark.parametrize("D", [128, 64, 96, 256])
 def test_noalloc_matches_workspace_entry_point(D, gpu):
     shapes = [(16, 1500, 3, 300), (8, 1100, 2, 100)]   # second call: smaller input
     for i, (T, P, H, n_txt) in enumerate(shapes):
