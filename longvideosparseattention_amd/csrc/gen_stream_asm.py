@@ -172,14 +172,11 @@ def lbl(name: str) -> str:
 
 
 class Gen:
-    def __init__(self, dt: str, D: int = 128, nw: int = 8, pad: bool = False, always_rare: bool = False,
-                 la: int | None = None,
-                 pv_b128: bool = False, no_softmax: bool = False, order: str = "group",
-                 no_barrier: bool = False, no_decode: bool = False, no_exp: bool = False,
-                 lead: int = 0, early_load: bool = False, no_mask: bool = False, dot_init: bool = False,
+    def __init__(self, dt: str, D: int = 128, nw: int = 8, always_rare: bool = False,
+                 la: int | None = None, order: str = "group",
+                 lead: int = 0, early_load: bool = False, dot_init: bool = False,
                  and_scc: bool = False, copy_split: bool = False, sm_start: int = 2, rs_mfma: bool = False,
-                 wait_pair: bool = False, rs_mix: bool = False, tail_nop: int = 12, no_switch: bool = False,
-                 no_fma: bool = False, qk_dup: bool = False, no_rare: bool = False, tail_split: bool = False,
+                 wait_pair: bool = False, rs_mix: bool = False, tail_nop: int = 12, tail_split: bool = False,
                  mask_fast: bool = False, mfma_order: str = "alt", copy_every: int = 2):
         assert dt in ("bf16", "f16")
         self.dt = dt
@@ -188,27 +185,16 @@ class Gen:
         self.wait_pair = wait_pair      # one LDS wait per two MFMAs (before the even one, for both)
         self.rs_mix = rs_mix            # rs_mfma softmax with the exponentials interleaved one by one
         self.tail_nop = tail_nop        # wait states between the last row-sum MFMA and its VALU read
-        self.no_switch = no_switch      # timing only (wrong with extra key rows): no key-source check
-        self.no_fma = no_fma            # timing only (wrong results): exp of S without scale and max
-        self.qk_dup = qk_dup            # timing only (wrong results): every QK MFMA issued twice
-        self.no_rare = no_rare          # timing only (wrong results): the rare-path branch never taken
         self.tail_split = tail_split    # rare test issued one MFMA before its branch
         self.mask_fast = mask_fast      # MASK: one lane mask for all 16 keys when the key split lies outside
         self.mfma_order = mfma_order    # QK / PV order in a sub-iteration: alternate, in pairs, or grouped
         self.copy_every = copy_every    # wide map: MFMAs between a block's copies
-        self.pad = pad                  # diagnostics: 16 wait states after every MFMA
         self.always_rare = always_rare  # diagnostics: exact row max on every sub-block
         self.la = (2 if nw == 12 else LA) if la is None else la   # MFMAs of LDS operand lookahead
         assert self.la < self.L.nslot
-        self.pv_b128 = pv_b128          # timing only (wrong results): one b128 read per PV operand
-        self.no_softmax = no_softmax    # timing only (wrong results): no softmax VALU
         self.order = order              # softmax op order: "group" (4 fma, 4 exp) or "mix"
-        self.no_barrier = no_barrier    # timing only (wrong results): no work-group barrier
-        self.no_decode = no_decode      # timing only (wrong results): copy sources not updated
-        self.no_exp = no_exp            # timing only (wrong results): no exponentials
         self.lead = lead                # PV MFMAs that open a block, their V operands read before the barrier
         self.early_load = early_load    # plan entry j+3 loaded in the middle of block j, not after it
-        self.no_mask = no_mask          # timing only (wrong results): masks not applied
         self.dot_init = dot_init        # row-sum chains start with v_dot2 (C = 0) instead of two v_mov
         self.and_scc = and_scc          # mask test branches on the SCC of s_and (no s_cmp)
         self.copy_split = copy_split    # M0 of a copy set one MFMA slot ahead (no s_nop)
@@ -232,17 +218,12 @@ class Gen:
     def softmax_ops(self, S: int, P: int) -> list[str]:
         """P = 2^(S*cs - m) as bf16/f16 pairs; this sub-block's row sum in LS0 + LS1."""
         L = self.L
-        if self.no_softmax:
-            return [f"v_mov_b32 {vr(L.LS0)}, 0", f"v_mov_b32 {vr(L.LS1)}, 0"]
         cvt = "v_cvt_pk_bf16_f32" if self.dt == "bf16" else "v_cvt_pk_f16_f32"
         one = "0x3f803f80" if self.dt == "bf16" else "0x3c003c00"
         dot = "v_dot2c_f32_bf16" if self.dt == "bf16" else "v_dot2c_f32_f16"
         t = lambda k: L.T + k % L.NT  # noqa: E731   (eight temporaries: groups g and g + 2 share)
         fma = lambda k: f"v_fma_f32 {vr(t(k))}, {vr(S + k)}, {sr(S_CS)}, -{vr(L.VM)}"  # noqa: E731
-        exp = lambda k: ("s_nop 0" if self.no_exp else f"v_exp_f32 {vr(t(k))}, {vr(t(k))}")  # noqa: E731
-        if self.no_fma:
-            fma = lambda k: None  # noqa: E731
-            exp = lambda k: f"v_exp_f32 {vr(t(k))}, {vr(S + k)}"  # noqa: E731
+        exp = lambda k: f"v_exp_f32 {vr(t(k))}, {vr(t(k))}"  # noqa: E731
         pk = lambda q: f"{cvt} {vr(P + q)}, {vr(t(2 * q))}, {vr(t(2 * q + 1))}"  # noqa: E731
         dot3 = "v_dot2_f32_bf16" if self.dt == "bf16" else "v_dot2_f32_f16"
 
@@ -273,7 +254,7 @@ class Gen:
                     if k == 11:
                         ops.append(rs(0))        # P + 0..3: packed by k = 8
                 ops += [pk(7), "s_nop 4", rs(1)]
-                return [o for o in ops if o is not None]
+                return ops
             for g in range(4):
                 ops += [fma(4 * g + i) for i in range(4)]
                 if g:
@@ -282,7 +263,7 @@ class Gen:
                 if g == 3:
                     ops.append(rs(0))            # P + 0..3 packed in groups 1 and 2
             ops += [pk(6), pk(7), "s_nop 4", rs(1)]   # VALU write -> MFMA read of the packs
-            return [o for o in ops if o is not None]
+            return ops
         ops = [] if self.dot_init else [f"v_mov_b32 {vr(L.LS0)}, 0", f"v_mov_b32 {vr(L.LS1)}, 0"]
         if self.order == "mix":
             # one exponential between two other ops: fma k+2, exp k; packs and dots
@@ -321,8 +302,8 @@ class Gen:
                     f"v_add_f32 {vr(L.LS0)}, {vr(L.LS0)}, {vr(L.LS1)}"]
         return head + [
                 f"v_cmp_nge_f32 vcc, 0x43800000, {vr(L.LS0)}",    # !(256 >= ls): ls > 256 or NaN
-                ("s_nop 0" if self.no_rare else
-                 f"s_branch {lbl('RSTUB_' + site)}" if self.always_rare else f"s_cbranch_vccnz {lbl('RSTUB_' + site)}"),
+                (f"s_branch {lbl('RSTUB_' + site)}" if self.always_rare else
+                 f"s_cbranch_vccnz {lbl('RSTUB_' + site)}"),
                 f"{lbl('RRET_' + site)}:",
                 f"v_add_f32 {vr(L.VL)}, {vr(L.VL)}, {vr(L.LS0)}"]
 
@@ -341,8 +322,6 @@ class Gen:
             fill.setdefault(at, []).extend(tail)
 
     def mask_check(self, site: str, sset: str, desc: int, half: int) -> list[str]:
-        if self.no_mask:
-            return []
         self.stubs += [f"{lbl('MSTUB_' + site)}:", f"s_mov_b32 s91, {sr(desc)}", f"s_mov_b32 s75, {32 * half}",
                        f"s_call_b64 {sr(S_RET, 2)}, {lbl('MASK_' + sset)}", f"s_branch {lbl('MRET_' + site)}"]
         test = [f"s_and_b32 s74, {sr(desc)}, 3"] + ([] if self.and_scc else ["s_cmp_lg_u32 s74, 0"])
@@ -440,10 +419,8 @@ class Gen:
         moves the soffsets; a change of source (video <-> extra rows) calls SWITCH."""
         self.stubs += [f"{lbl('SWSTUB_' + site)}:", f"s_call_b64 {sr(S_RET, 2)}, {lbl('SWITCH')}",
                        f"s_branch {lbl('SWRET_' + site)}"]
-        # (no_switch keeps the check in the setup decodes, sites S0 / S1, which load
-        # the buffer resources of the first block's source)
-        chk = [] if (self.no_switch and not site.startswith("S")) else [
-            f"s_lshr_b32 s74, {sr(x)}, 31", f"s_cmp_lg_u32 s74, {sr(S_CUR)}", f"s_cbranch_scc1 {lbl('SWSTUB_' + site)}"]
+        chk = [f"s_lshr_b32 s74, {sr(x)}, 31", f"s_cmp_lg_u32 s74, {sr(S_CUR)}",
+               f"s_cbranch_scc1 {lbl('SWSTUB_' + site)}"]
         r = chk + [
             f"{lbl('SWRET_' + site)}:",
             f"s_and_b32 s73, {sr(x)}, 0x7fffffff",
@@ -570,7 +547,7 @@ class Gen:
         seq = list(mfmas) + list(nxt)
         n, nn = len(mfmas), len(seq)
         LA = self.la
-        nreads = [1 if (m[0] == "qk" or self.pv_b128) else 2 for m in seq]
+        nreads = [1 if m[0] == "qk" else 2 for m in seq]
 
         def reads(i: int) -> list[str]:
             m = seq[i]
@@ -580,8 +557,6 @@ class Gen:
                 return [f"ds_read_b128 {vr(slot, 4)}, {vr(L.KOFF + c)} offset:{st * L.TILE + half * 32 * L.RB}"]
             _, st, st16, dt, _ = m
             off = st * L.TILE + st16 * 16 * L.RB    # the V^T read offsets include VBASE
-            if self.pv_b128:
-                return [f"ds_read_b128 {vr(slot, 4)}, {vr(L.KOFF + dt)} offset:{off}"]
             return [f"ds_read_b64_tr_b16 {vr(slot, 2)}, {vr(L.VOFFA + dt)} offset:{off}",
                     f"ds_read_b64_tr_b16 {vr(slot + 2, 2)}, {vr(L.VOFFB + dt)} offset:{off}"]
 
@@ -607,14 +582,10 @@ class Gen:
             if m[0] == "qk":
                 _, _, _, c, S = m
                 self.e(f"{self.mfma} {vr(S, 16)}, {vr(slot, 4)}, {vr(L.Q + 4 * c, 4)}, {'0' if c == 0 else vr(S, 16)}")
-                if self.qk_dup:
-                    self.e(f"{self.mfma} {vr(S, 16)}, {vr(slot, 4)}, {vr(L.Q + 4 * c, 4)}, {vr(S, 16)}")
             else:
                 _, _, st16, dt, P = m
                 acc = self.ov(L.O + 16 * dt, 16)
                 self.e(f"{self.mfma} {acc}, {vr(slot, 4)}, {vr(P + 4 * (st16 & 1), 4)}, {acc}")
-            if self.pad:
-                self.e("s_nop 15")
             while issued < min(nn, i + 1 + LA):
                 self.e(*reads(issued))
                 issued += 1
@@ -659,7 +630,7 @@ class Gen:
         site = f"I{stage}"
         M = 2 * L.NQK                     # MFMAs per sub-iteration (QK and PV interleaved)
         self.e(f"; ── block j, K stage {stage}", f"s_waitcnt vmcnt({0 if L.wide else 2 * L.NCP})",
-               "s_nop 0" if self.no_barrier else "s_barrier", "s_waitcnt lgkmcnt(0)")
+               "s_barrier", "s_waitcnt lgkmcnt(0)")
         mf = []
         half_q = L.NQK // 2               # QK k-steps per 16-key PV step
         for half, S, P in ((0, L.SA, L.PA), (1, L.SB, L.PB)):
@@ -678,12 +649,12 @@ class Gen:
         assert mf[:len(self.lead_pv(vst))] == self.lead_pv(vst)
         if L.wide:
             # K(j+1) into the K stage K(j-1) left, V(j) into the V stage V(j-2) left
-            fill = {0: [] if self.no_decode else (self.decode_wide(S_ENT + 2 * ((stage + 1) & 3), site, False) +
-                                                  self.decode_wide(S_ENT + 2 * stage, site, True))}
+            fill = {0: self.decode_wide(S_ENT + 2 * ((stage + 1) & 3), site, False) +
+                    self.decode_wide(S_ENT + 2 * stage, site, True)}
             for k in range(2 * L.NCP):
                 self.place_copy(fill, 1 + self.copy_every * k, (stage + 1) & 1 if k < L.NCP else stage & 1, k)
         else:
-            fill = {0: [] if self.no_decode else self.decode(S_ENT + 2 * cst, site)}
+            fill = {0: self.decode(S_ENT + 2 * cst, site)}
             # copies after MFMAs spread over the block's 4*NQK MFMAs
             at_copy = {8: (6, 10, 22, 26), 6: (4, 8, 16, 20), 4: (5, 13)}[L.NQK]
             for k, at in enumerate(at_copy):
