@@ -278,10 +278,12 @@ def main(argv=None) -> int:
     tag = args.config + ("" if args.window is None else f"_w{W}") + (
         "" if args.head_dim is None or args.head_dim == CONFIGS[args.config][3] else f"_d{D}")
     traffic, traffic_src, traffic_note = profiled_traffic(tag)
-    kernel = {128: "attn_fwd_stream_kernel", 64: "attn_fwd_stream_kernel", 96: "attn_fwd_stream_kernel"}.get(
-        D, "attn_fwd_kernel")
-    if D in (64, 96, 128) and os.environ.get("LVSA_ATTN_KERNEL") == "pp":
-        kernel = "attn_fwd_pp_kernel"
+    # every 16-bit head size runs the single-stream kernel on these geometries
+    # (D = 192 and 256 in its wide map); LVSA_ATTN_KERNEL=pp selects the
+    # ping-pong kernel (D <= 128) or the 4-wave kernel (D >= 192)
+    kernel = "attn_fwd_stream_kernel"
+    if os.environ.get("LVSA_ATTN_KERNEL") == "pp":
+        kernel = "attn_fwd_pp_kernel" if D <= 128 else "attn_fwd_kernel"
     if dname == "f32":
         kernel = "attn_fwd_f32_kernel"
 
