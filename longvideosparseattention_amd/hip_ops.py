@@ -37,8 +37,9 @@ def attn_block_q(head_dim: int = 128, dtype: Optional[torch.dtype] = None, frame
     and key frames at least 64 (``frame_rows``, ``key_rows``): the 12-wave
     single-stream kernel, three waves per SIMD.  256 for head sizes 64, 96
     and 128 otherwise: the 8-wave kernels (bf16 / fp16).  128 for 192 and 256:
-    the 4-wave kernel (the 8-wave kernels' registers hold no Q and O that
-    wide), and for fp32 inputs at every head size (the fp32 kernel).
+    the single-stream kernel's wide map (4 waves, one per SIMD, when query
+    frames span at least 127 rows and key frames at least 64) or else the
+    4-wave kernel, and for fp32 inputs at every head size (the fp32 kernel).
     ``LVSA_ATTN_BLOCK_Q`` (128, 256 or 384) overrides the choice for 64 and 128
     in 16-bit (384: head size 64 only); 96 runs on the 8-wave kernel only."""
     kd = kernel_head_dim(head_dim)
