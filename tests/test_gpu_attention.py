@@ -510,6 +510,63 @@ def test_baseline_sweep_spot_frames(cfg, gpu):
             _close(ot, rto, f"{name} text rows")
 
 
+SUPPORT = [
+    # name, T, P, W, kfi, H, D, n_txt, offsets (full BASELINE sizes, bf16; T + 1 <= D)
+    ("wan4x", 84, 1560, 2, 8, 12, 128, 0, tuple(range(8))),
+    ("wan6x_w0", 121, 1560, 0, 8, 12, 128, 0, (2,)),
+    ("wan6x_w1", 121, 1560, 1, 8, 12, 128, 0, (3,)),
+    ("wan6x_w2", 121, 1560, 2, 8, 12, 128, 0, (0, 5)),
+    ("wan6x_w3", 121, 1560, 3, 8, 12, 128, 0, (6,)),
+    ("wan6x_w4", 121, 1560, 4, 8, 12, 128, 0, (1, 7)),
+    ("cog", 13, 1350, 1, 4, 48, 64, 226, tuple(range(4))),
+    ("hv", 49, 1590, 2, 8, 16, 128, 256, tuple(range(8))),
+]
+
+
+@pytest.mark.parametrize("cfg", SUPPORT, ids=[c[0] for c in SUPPORT])
+def test_baseline_frame_support_every_row(cfg, gpu):
+    """Every query row at full size, every listed keyframe rotation: with the
+    value rows of key frame t equal to the unit vector e_t (text keys: e_T),
+    output coordinate d of a row is the softmax weight its row gives key
+    frame d.  So a row's nonzero coordinates must be exactly the frames the
+    reference's frame rule lets its query frame attend (plus the text
+    keys), each weight positive, every other coordinate exactly 0 (masked
+    keys and skipped blocks contribute nothing), and the weights sum to 1.
+    Text-query rows attend every frame and the text."""
+    name, T, P, W, kfi, H, D, n_txt, offsets = cfg
+    assert T + 1 <= D
+    N = T * P
+    g = torch.Generator(device=gpu).manual_seed(29)
+    q, k = (torch.randn(1, N, H, D, generator=g, device=gpu).to(torch.bfloat16) for _ in range(2))
+    fidx = torch.arange(N, device=gpu) // P
+    v = torch.zeros(1, N, H, D, device=gpu, dtype=torch.bfloat16)
+    v[0, torch.arange(N, device=gpu), :, fidx] = 1.0
+    args = {}
+    if n_txt:
+        qt, kt = (torch.randn(1, n_txt, H, D, generator=g, device=gpu).to(torch.bfloat16) for _ in range(2))
+        vt = torch.zeros(1, n_txt, H, D, device=gpu, dtype=torch.bfloat16)
+        vt[..., T] = 1.0
+        args = dict(k_text=kt, v_text=vt, q_text=qt)
+    for off in offsets:
+        m = _meta(T, P, W, 1, kfi, off)
+        res = lv.lvsa_attention(q, k, v, m, **args)
+        o = (res[0] if n_txt else res)[0].float()                    # [N, H, D]
+        allowed = torch.zeros(T, D, dtype=torch.bool)
+        for i, r in enumerate(om.build_frame_mask(T, P, W, 1, kfi, offset=off).rows):
+            allowed[i, sorted(r)] = True
+        if n_txt:
+            allowed[:, T] = True
+        keep = allowed.to(gpu)[fidx][:, None, :]                      # [N, 1, D]
+        what = f"{name} offset {off}"
+        assert o.masked_fill(keep, 0.0).abs().max().item() == 0.0, what + ": weight on a frame outside the rule"
+        assert o.masked_fill(~keep, 1.0).min().item() > 1e-4, what + ": an allowed frame got no weight"
+        assert (o.sum(-1) - 1.0).abs().max().item() < 1e-2, what + ": weights do not sum to 1"
+        if n_txt:
+            ot = res[1][0].float()
+            assert ot[..., T + 1:].abs().max().item() == 0.0 and ot[..., :T + 1].min().item() > 1e-4, what
+            assert (ot.sum(-1) - 1.0).abs().max().item() < 1e-2, what
+
+
 SPLIT = [
     # T, P, H, Hkv, D, n_txt, dtype, B   (text tiles of more than 128 key blocks: split into chunks)
     (8, 1100, 2, 2, 128, 100, torch.bfloat16, 1),   # 141 blocks: 2 chunks
