@@ -1,17 +1,20 @@
-// Kernels of the block-sparse attention forward (gfx950), shared by the
-// translation units that instantiate them: lvsa_attn.hip (C ABI, D = 64 and
-// 256), lvsa_attn_d128.hip (D = 128, built with the max-ILP machine
-// scheduler, which schedules the D = 128 ping-pong loop about 2% faster and
-// the D = 64 one slower), lvsa_attn_d96.hip (D = 96) and lvsa_attn_d192.hip
-// (D = 192).
+// Compiler-built kernels of the block-sparse attention forward (gfx950) and
+// what they share with the hand-scheduled single-stream kernel
+// (lvsa_attn_stream.h): parameters, plan entries, work queues, the text
+// split.  One translation unit per head size instantiates them
+// (lvsa_attn_d{64,96,128,192,256}.hip, each with the machine scheduler
+// measured fastest for it; lvsa_attn.hip holds the C ABI).
 //
-// Two kernels walk the key blocks (BN = 64 rows each) that the block plan
-// lists for a query tile of one head:
+// Two kernels here walk the key blocks (BN = 64 rows each) that the block
+// plan lists for a query tile of one head; they serve the geometries the
+// single-stream kernel does not take (frames too short for it) and the
+// LVSA_ATTN_KERNEL=pp comparison:
 //   attn_fwd_pp_kernel   256-row tiles, 8 waves x 32 rows in two groups that
 //                        alternate an MFMA phase with a softmax phase (D = 64,
-//                        96 and 128; the default);
+//                        96 and 128);
 //   attn_fwd_kernel      128-row tiles, 4 waves x 32 rows, one barrier per
-//                        block (D = 256, whose Q and O need 320 registers).
+//                        block (D = 192 and 256, whose Q and O need 320
+//                        registers; any head size with LVSA_ATTN_BLOCK_Q=128).
 // Both compute, per wave and key block:
 //   S^T = K · Q^T      v_mfma_f32_32x32x16_{bf16,f16}: A = K rows from LDS
 //                      (ds_read_b128), B = Q held in registers for the tile
