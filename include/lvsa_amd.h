@@ -149,7 +149,7 @@ typedef struct lvsa_plan_params {
   int32_t q_frame0;
   int32_t rel_rows, words;
   const uint32_t* rel;      /* device bitmap [rel_rows*words]                     */
-  int32_t block_q, block_k; /* attention kernel: 128 x 64                         */
+  int32_t block_q, block_k; /* query tile rows (128/256/384) x key block (64)     */
 } lvsa_plan_params;
 
 typedef struct lvsa_plan_sizes {
@@ -201,8 +201,9 @@ typedef struct lvsa_attn_args {
   int32_t n_q, n_k, n_x, n_tq;
   float scale;              /* softmax scale (reference: 1/sqrt(D))             */
   int32_t dtype;            /* lvsa_dtype                                       */
-  /* plan (built with block_q = 128 or 256 query rows and block_k = 64;
-   * D = 192 and 256 run 128-row tiles only, D = 96 256-row tiles only) */
+  /* plan (built with block_q = 128, 256 or 384 query rows and block_k = 64;
+   * D = 192 and 256 and fp32 run 128-row tiles only, D = 96 256-row tiles
+   * only, 384-row tiles are for D = 64 in 16 bit) */
   int32_t block_q;
   const int32_t* tile_indptr;
   const uint32_t* entries;

@@ -261,7 +261,8 @@ extern "C" int lvsa_attn_fwd(const lvsa_attn_args* a, hipStream_t stream) {
   p.text_chunks = chunks;
   p.text_first = chunks == 1 ? 1 : 0;
   p.ws = chunks > 1 ? (float*)a->workspace : nullptr;
-  // The single-stream kernel (D = 64, 96 and 128 here) serves plans without generic descriptors:
+  // The single-stream kernel (D = 64, 96 and 128 here; 192 and 256 below)
+  // serves plans without generic descriptors:
   // 256-row tiles touch at most two query frames when frames have >= 255
   // rows, and 64-key blocks (even short last ones) at most two key frames
   // when frames have >= 64 keys.  LVSA_ATTN_KERNEL=pp selects the ping-pong
@@ -269,9 +270,9 @@ extern "C" int lvsa_attn_fwd(const lvsa_attn_args* a, hipStream_t stream) {
   const char* kenv = getenv("LVSA_ATTN_KERNEL");
   const bool force_pp = kenv != nullptr && strcmp(kenv, "pp") == 0;
   // Its copies address a whole key source through one buffer resource with
-  // 32-bit byte offsets; at D = 96 the lanes of the unused chunks of a row add
-  // 0x7FFF0000 to theirs (out of range: zeros, no access), so the rows must
-  // stay below 2^31 bytes there.
+  // 32-bit byte offsets; at D = 96 and 192 the lanes of the unused chunks of
+  // a row add 0x7FFF0000 to theirs (out of range: zeros, no access), so the
+  // rows must stay below 2^31 bytes there.
   const int64_t lim = (a->D == 96 || a->D == 192) ? (1LL << 31) : (1LL << 32);
   auto fits32 = [lim](int64_t rows, int64_t row_elems) { return (rows + kBN) * row_elems * 2 < lim; };
   const bool src32 = fits32(a->n_k, a->k_str[1]) && fits32(a->n_k, a->v_str[1]) &&
