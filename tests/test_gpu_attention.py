@@ -510,6 +510,40 @@ def test_baseline_sweep_spot_frames(cfg, gpu):
             _close(ot, rto, f"{name} text rows")
 
 
+ALL_FRAMES = [
+    # name, T, P, W, kfi, off, H, D, n_txt (full BASELINE sizes, bf16, one offset each)
+    ("wan4x_off3", 84, 1560, 2, 8, 3, 12, 128, 0),
+    ("wan6x_w2_off4", 121, 1560, 2, 8, 4, 12, 128, 0),
+    ("hv_off5", 49, 1590, 2, 8, 5, 16, 128, 256),
+    ("cog_off1", 13, 1350, 1, 4, 1, 48, 64, 226),
+]
+
+
+@pytest.mark.parametrize("cfg", ALL_FRAMES, ids=[c[0] for c in ALL_FRAMES])
+def test_baseline_all_frames(cfg, gpu):
+    """Every query frame (not a sample) at full size against the fp32 oracle
+    (its per-frame gather and dense attention run on the GPU in fp32), with
+    the LSE; text rows too."""
+    name, T, P, W, kfi, off, H, D, n_txt = cfg
+    N = T * P
+    g = torch.Generator(device=gpu).manual_seed(37)
+    q, k, v = (torch.randn(1, N, H, D, generator=g, device=gpu).to(torch.bfloat16) for _ in range(3))
+    qt, kt, vt = (torch.randn(1, n_txt, H, D, generator=g, device=gpu).to(torch.bfloat16) for _ in range(3))
+    m = _meta(T, P, W, 1, kfi, off)
+    args = dict(k_text=kt, v_text=vt, q_text=qt) if n_txt else {}
+    res = lv.lvsa_attention(q, k, v, m, return_lse=True, **args)
+    o, lse = (res[0], res[2]) if n_txt else res
+    rows = [set(r) for r in om.build_frame_mask(T, P, W, 1, kfi, offset=off).rows]
+    ro, rl = oa.per_frame_sdpa(q.float(), k.float(), v.float(), rows, P, k_extra=kt.float() if n_txt else None,
+                               v_extra=vt.float() if n_txt else None)
+    assert not torch.isnan(ro).any()
+    _close(o, ro, name)
+    torch.testing.assert_close(lse.float(), rl, atol=2e-2, rtol=0, msg=name)
+    if n_txt:
+        rto, _ = oa.text_row_attention(qt.float(), k.float(), v.float(), kt.float(), vt.float())
+        _close(res[1], rto, name + " text rows")
+
+
 SUPPORT = [
     # name, T, P, W, kfi, H, D, n_txt, offsets (full BASELINE sizes, bf16; T + 1 <= D)
     ("wan4x", 84, 1560, 2, 8, 12, 128, 0, tuple(range(8))),
