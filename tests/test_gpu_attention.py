@@ -516,6 +516,10 @@ ALL_FRAMES = [
     ("wan6x_w2_off4", 121, 1560, 2, 8, 4, 12, 128, 0),
     ("hv_off5", 49, 1590, 2, 8, 5, 16, 128, 256),
     ("cog_off1", 13, 1350, 1, 4, 1, 48, 64, 226),
+    # the plugin's other head sizes at the Wan 4x geometry (96: D = 128 LDS layout; 192, 256: wide map)
+    ("wan4x_d96_off6", 84, 1560, 2, 8, 6, 12, 96, 0),
+    ("wan4x_d192_off1", 84, 1560, 2, 8, 1, 12, 192, 0),
+    ("wan4x_d256_off7", 84, 1560, 2, 8, 7, 12, 256, 0),
 ]
 
 
