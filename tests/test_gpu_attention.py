@@ -511,7 +511,7 @@ def test_baseline_sweep_spot_frames(cfg, gpu):
 
 
 ALL_FRAMES = [
-    # name, T, P, W, kfi, off, H, D, n_txt (full BASELINE sizes, bf16, one offset each)
+    # name, T, P, W, kfi, off, H, D, n_txt[, dtype] (full BASELINE sizes, bf16 unless given, one offset each)
     ("wan4x_off3", 84, 1560, 2, 8, 3, 12, 128, 0),
     ("wan6x_w2_off4", 121, 1560, 2, 8, 4, 12, 128, 0),
     ("hv_off5", 49, 1590, 2, 8, 5, 16, 128, 256),
@@ -520,6 +520,9 @@ ALL_FRAMES = [
     ("wan4x_d96_off6", 84, 1560, 2, 8, 6, 12, 96, 0),
     ("wan4x_d192_off1", 84, 1560, 2, 8, 1, 12, 192, 0),
     ("wan4x_d256_off7", 84, 1560, 2, 8, 7, 12, 256, 0),
+    # fp16 inputs (the loops' f16 variants)
+    ("wan4x_f16_off0", 84, 1560, 2, 8, 0, 12, 128, 0, torch.float16),
+    ("cog_f16_off2", 13, 1350, 1, 4, 2, 48, 64, 226, torch.float16),
 ]
 
 
@@ -528,11 +531,12 @@ def test_baseline_all_frames(cfg, gpu):
     """Every query frame (not a sample) at full size against the fp32 oracle
     (its per-frame gather and dense attention run on the GPU in fp32), with
     the LSE; text rows too."""
-    name, T, P, W, kfi, off, H, D, n_txt = cfg
+    name, T, P, W, kfi, off, H, D, n_txt = cfg[:9]
+    dt = cfg[9] if len(cfg) > 9 else torch.bfloat16
     N = T * P
     g = torch.Generator(device=gpu).manual_seed(37)
-    q, k, v = (torch.randn(1, N, H, D, generator=g, device=gpu).to(torch.bfloat16) for _ in range(3))
-    qt, kt, vt = (torch.randn(1, n_txt, H, D, generator=g, device=gpu).to(torch.bfloat16) for _ in range(3))
+    q, k, v = (torch.randn(1, N, H, D, generator=g, device=gpu).to(dt) for _ in range(3))
+    qt, kt, vt = (torch.randn(1, n_txt, H, D, generator=g, device=gpu).to(dt) for _ in range(3))
     m = _meta(T, P, W, 1, kfi, off)
     args = dict(k_text=kt, v_text=vt, q_text=qt) if n_txt else {}
     res = lv.lvsa_attention(q, k, v, m, return_lse=True, **args)
