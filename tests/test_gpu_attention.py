@@ -511,7 +511,8 @@ def test_baseline_sweep_spot_frames(cfg, gpu):
 
 
 ALL_FRAMES = [
-    # name, T, P, W, kfi, off, H, D, n_txt[, dtype] (full BASELINE sizes, bf16 unless given, one offset each)
+    # name, T, P, W, kfi, off, H, D, n_txt[, dtype[, Hkv]] (full BASELINE sizes, bf16 and Hkv = H unless
+    # given, one offset each)
     ("wan4x_off3", 84, 1560, 2, 8, 3, 12, 128, 0),
     ("wan6x_w2_off4", 121, 1560, 2, 8, 4, 12, 128, 0),
     ("hv_off5", 49, 1590, 2, 8, 5, 16, 128, 256),
@@ -523,6 +524,8 @@ ALL_FRAMES = [
     # fp16 inputs (the loops' f16 variants)
     ("wan4x_f16_off0", 84, 1560, 2, 8, 0, 12, 128, 0, torch.float16),
     ("cog_f16_off2", 13, 1350, 1, 4, 2, 48, 64, 226, torch.float16),
+    # grouped K/V heads (3 query heads per K/V head), read in place
+    ("wan4x_gqa3_off2", 84, 1560, 2, 8, 2, 12, 128, 0, torch.bfloat16, 4),
 ]
 
 
@@ -533,10 +536,13 @@ def test_baseline_all_frames(cfg, gpu):
     the LSE; text rows too."""
     name, T, P, W, kfi, off, H, D, n_txt = cfg[:9]
     dt = cfg[9] if len(cfg) > 9 else torch.bfloat16
+    Hkv = cfg[10] if len(cfg) > 10 else H
     N = T * P
     g = torch.Generator(device=gpu).manual_seed(37)
-    q, k, v = (torch.randn(1, N, H, D, generator=g, device=gpu).to(dt) for _ in range(3))
-    qt, kt, vt = (torch.randn(1, n_txt, H, D, generator=g, device=gpu).to(dt) for _ in range(3))
+    q = torch.randn(1, N, H, D, generator=g, device=gpu).to(dt)
+    k, v = (torch.randn(1, N, Hkv, D, generator=g, device=gpu).to(dt) for _ in range(2))
+    qt = torch.randn(1, n_txt, H, D, generator=g, device=gpu).to(dt)
+    kt, vt = (torch.randn(1, n_txt, Hkv, D, generator=g, device=gpu).to(dt) for _ in range(2))
     m = _meta(T, P, W, 1, kfi, off)
     args = dict(k_text=kt, v_text=vt, q_text=qt) if n_txt else {}
     res = lv.lvsa_attention(q, k, v, m, return_lse=True, **args)
