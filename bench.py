@@ -259,21 +259,29 @@ def main(argv=None) -> int:
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
-    # events on the stream the kernels are launched on (torch's current stream)
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # events on the stream the kernels are launched on (torch's current
+    # stream), one between consecutive calls: per-call times without a host
+    # synchronisation inside the timed region
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     t0 = time.perf_counter()
-    ev0.record()
+    evs[0].record()
     for i in range(args.steps):
         step(i)
-    ev1.record()
+        evs[i + 1].record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    ev_ms = ev0.elapsed_time(ev1) / args.steps
+    call_ms = [evs[i].elapsed_time(evs[i + 1]) for i in range(args.steps)]
+    ev_ms = evs[0].elapsed_time(evs[-1]) / args.steps
+    ev_median = sorted(call_ms)[args.steps // 2] if args.steps % 2 else \
+        0.5 * sum(sorted(call_ms)[args.steps // 2 - 1:args.steps // 2 + 1])
     ms = 1e3 * wall / args.steps
     fb = sum(flops[offsets[i % len(offsets)]][0] for i in range(args.steps))
     fx = sum(flops[offsets[i % len(offsets)]][1] for i in range(args.steps))
     value = fb / wall / 1e12
     achieved = fb / (ev_ms * 1e-3 * args.steps) / 1e12
+    per_call_tf = sorted(flops[offsets[i % len(offsets)]][0] / (call_ms[i] * 1e-3) / 1e12 for i in range(args.steps))
+    achieved_median = per_call_tf[args.steps // 2] if args.steps % 2 else \
+        0.5 * (per_call_tf[args.steps // 2 - 1] + per_call_tf[args.steps // 2])
     bytes_per_call = 4 * (N + n_text) * H * D * 2
     tag = args.config + ("" if args.window is None else f"_w{W}") + (
         "" if args.head_dim is None or args.head_dim == CONFIGS[args.config][3] else f"_d{D}")
@@ -296,6 +304,9 @@ def main(argv=None) -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms, 4),
+        # median of the per-call HIP-event times (the keyframe offset rotates,
+        # so calls differ in work by a few percent)
+        "ms_per_call_median": round(ev_median, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -319,7 +330,9 @@ def main(argv=None) -> int:
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak,
                      "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": traffic,
                      "traffic_source": traffic_src, "traffic_note": traffic_note, "kernel": kernel,
-                     "event_ms_per_call": round(ev_ms, 4), "build": source_hash()},
+                     "event_ms_per_call": round(ev_ms, 4), "event_ms_per_call_median": round(ev_median, 4),
+                     "event_ms_per_call_min_max": [round(min(call_ms), 4), round(max(call_ms), 4)],
+                     "achieved_median": round(achieved_median, 2), "build": source_hash()},
     }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(q.float().cpu(), k.float().cpu(), v.float().cpu(),

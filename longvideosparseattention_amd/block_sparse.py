@@ -129,6 +129,23 @@ class BlockSparseAttentionWrapper:
         return o, lse2
 
 
+    def run_batched(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+        """``run`` over a batch in one launch: ``q [B, M, H, D]``, ``k``/``v``
+        ``[B, N, H_kv, D]`` → ``o [B, M, H, D]``.  Every batch element uses the
+        planned block pattern (the kernel's batch index is a grid dimension)."""
+        if self._plan is None:
+            raise RuntimeError("plan() must be called before run()")
+        M, N, H, Hkv, D = self._shape
+        B = q.shape[0]
+        if q.shape != (B, M, H, D) or k.shape != (B, N, Hkv, D) or v.shape != (B, N, Hkv, D):
+            raise ValueError(f"run_batched() shapes {tuple(q.shape)}, {tuple(k.shape)} do not match the plan "
+                             f"{self._shape} with a leading batch")
+        self._check_columns()
+        self._plan = self._plan_for(D, q.dtype)
+        o, _, _, _ = hip_ops.attn_fwd(q, k, v, self._plan, scale=self._scale)
+        return o
+
+
 _DENSE_PLANS = {}
 
 

@@ -32,6 +32,7 @@ MAXOCC = ["-mllvm", "-amdgpu-sched-strategy=iterative-maxocc"]
 SOURCES = {
     "lvsa_mask.hip": [],
     "lvsa_attn.hip": [],
+    "lvsa_noalloc.hip": [],
     "lvsa_attn_d64.hip": [],
     "lvsa_attn_d96.hip": [],
     "lvsa_attn_d128.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"],

@@ -1,6 +1,7 @@
 """Generate the key loop of the single-stream attention kernel (every 16-bit head size).
 
     python gen_stream_asm.py [out.inc]   (default: lvsa_attn_stream_body.inc beside this file)
+    python gen_stream_asm.py --census    (instruction counts per 32-key sub-block of each loop)
 
 The loop is hand-scheduled gfx950 assembly, emitted as the body of one inline
 asm statement of ``attn_fwd_stream_kernel`` (lvsa_attn_stream.h), whose
@@ -840,8 +841,65 @@ def render(per_d: dict | None = None, **opts) -> str:
     return "\n".join(out)
 
 
+CENSUS_KINDS = ("mfma 32x32x16", "mfma 16x16x32", "valu", "of which v_exp", "lds", "vmem copy", "salu",
+                "smem", "branch", "barrier", "s_waitcnt", "s_nop states")
+
+
+def census(D: int, nw: int, dt: str = "bf16") -> dict:
+    """Instruction counts per 32-key sub-block of the steady-state loop (the
+    four unrolled blocks between LOOP and its back branch) of the product's
+    loop for (D, nw): the common path, without the subroutines a masked
+    block or the rare case calls."""
+    lines = Gen(dt, D=D, nw=nw, **PRODUCT[D]).build()
+    a = next(i for i, x in enumerate(lines) if x.startswith("LOOP_"))
+    b = next(i for i, x in enumerate(lines) if x.startswith("s_branch LOOP_"))
+    c = dict.fromkeys(CENSUS_KINDS, 0)
+    for ln in lines[a + 1:b]:
+        op = ln.split()[0] if ln and not ln.startswith(";") and not ln.endswith(":") else ""
+        if not op:
+            continue
+        if op.startswith("v_mfma_f32_32x32"):
+            c["mfma 32x32x16"] += 1
+        elif op.startswith("v_mfma_f32_16x16"):
+            c["mfma 16x16x32"] += 1
+        elif op.startswith("v_"):
+            c["valu"] += 1
+            c["of which v_exp"] += op.startswith("v_exp")
+        elif op.startswith("ds_"):
+            c["lds"] += 1
+        elif op.startswith("buffer_"):
+            c["vmem copy"] += 1
+        elif op == "s_barrier":
+            c["barrier"] += 1
+        elif op == "s_waitcnt":
+            c["s_waitcnt"] += 1
+        elif op == "s_nop":
+            c["s_nop states"] += int(ln.split()[1]) + 1
+        elif op.startswith(("s_cbranch", "s_branch", "s_call", "s_setpc")):
+            c["branch"] += 1
+        elif op.startswith(("s_load", "s_buffer_load")):
+            c["smem"] += 1
+        elif op.startswith("s_"):
+            c["salu"] += 1
+        else:
+            raise ValueError(f"census: unclassified instruction {ln!r}")
+    return {k: v / 8 for k, v in c.items()}          # 4 blocks x 2 sub-blocks
+
+
+def print_census() -> None:
+    cols = [(128, 8), (96, 8), (64, 12), (64, 8), (192, 4), (256, 4)]
+    res = {col: census(*col) for col in cols}
+    print("| per 32-key sub-block, per wave | " + " | ".join(f"D={d}, {n} waves" for d, n in cols) + " |")
+    print("|---|" + "---|" * len(cols))
+    for k in CENSUS_KINDS:
+        print(f"| {k} | " + " | ".join(f"{res[col][k]:g}" for col in cols) + " |")
+
+
 def main(argv=None) -> int:
     argv = sys.argv[1:] if argv is None else argv
+    if argv and argv[0] == "--census":
+        print_census()
+        return 0
     dst = Path(argv[0]) if argv else Path(__file__).with_name("lvsa_attn_stream_body.inc")
     text = render()
     if not dst.exists() or dst.read_text() != text:

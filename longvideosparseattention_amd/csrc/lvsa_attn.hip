@@ -101,30 +101,17 @@ __global__ __launch_bounds__(256) void attn_text_merge_kernel(const float* ws, i
     lse_t[bh * n_tq + row] = L > 0.f ? (M + __log2f(L)) * 0.69314718055994530942f : -INFINITY;
 }
 
-// Scratch of lvsa_attn_fwd_noalloc: one array per GPU, held by the loaded
-// code object until the process ends.  In host code `scratch` only names the
-// symbol; its device address comes from hipGetSymbolAddress, once per device.
-__device__ __align__(256) char scratch[LVSA_NOALLOC_SCRATCH_BYTES];
-constexpr int kMaxDevices = 64;
-std::mutex g_scratch_mu;
-void* g_scratch_ptr[kMaxDevices] = {};
-
-// Device address of the current device's scratch (set up on its first call).
-int scratch_of_current_device(void** out) {
-  int dev = -1;
-  hipError_t e = hipGetDevice(&dev);
-  LVSA_REQUIRE(e == hipSuccess, LVSA_ERR_HIP, "lvsa_attn_fwd_noalloc: hipGetDevice: %s", hipGetErrorString(e));
-  LVSA_REQUIRE(dev >= 0 && dev < kMaxDevices, LVSA_ERR_UNSUPPORTED, "lvsa_attn_fwd_noalloc: device %d", dev);
-  std::lock_guard<std::mutex> lock(g_scratch_mu);
-  if (g_scratch_ptr[dev] == nullptr) {
-    void* ptr = nullptr;
-    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
-    LVSA_REQUIRE(e == hipSuccess && ptr != nullptr, LVSA_ERR_HIP,
-                 "lvsa_attn_fwd_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
-    g_scratch_ptr[dev] = ptr;
-  }
-  *out = g_scratch_ptr[dev];
-  return LVSA_OK;
+// Whether the short last key block of the frame-structured source crosses a
+// frame boundary: it holds the t = n_k - 64 floor((n_k - 1) / 64) < 64 last
+// keys, tokens [k_tok0 + n_k - t, k_tok0 + n_k), and the last boundary at or
+// below its end lies e = (k_tok0 + n_k) mod C tokens before that end.  The
+// plan builder describes such a block as "generic" (two frames and the rows
+// past the end of the source).
+bool stream_tail_crosses_frame(int64_t n_q, int64_t n_k, int64_t k_tok0, int C) {
+  if (n_q == 0 || n_k <= 0 || C <= 0) return false;
+  const int64_t t = n_k - kBN * ((n_k - 1) / kBN);
+  const int64_t e = (k_tok0 + n_k) % C;
+  return t < kBN && e > 0 && e < t;
 }
 
 bool aligned16(const void* ptr, const int64_t* str, int n, int elem_bytes) {
@@ -271,23 +258,38 @@ extern "C" int lvsa_attn_fwd(const lvsa_attn_args* a, hipStream_t stream) {
   const bool force_pp = kenv != nullptr && strcmp(kenv, "pp") == 0;
   // Its copies address a whole key source through one buffer resource with
   // 32-bit byte offsets; at D = 96 and 192 the lanes of the unused chunks of
-  // a row add 0x7FFF0000 to theirs (out of range: zeros, no access), so the
-  // rows must stay below 2^31 bytes there.
+  // a row add 0x7FFF0000 to theirs, which must lie past the end of the
+  // source (zeros, no access) or inside it (a harmless read into chunks no
+  // read touches): the rows must stay below 2^31 bytes there.
   const int64_t lim = (a->D == 96 || a->D == 192) ? (1LL << 31) : (1LL << 32);
   auto fits32 = [lim](int64_t rows, int64_t row_elems) { return (rows + kBN) * row_elems * 2 < lim; };
   const bool src32 = fits32(a->n_k, a->k_str[1]) && fits32(a->n_k, a->v_str[1]) &&
                      (a->n_x == 0 || (fits32(a->n_x, a->kx_str[1]) && fits32(a->n_x, a->vx_str[1])));
-  p.use_stream = (!fp32 && (a->D == 128 || a->D == 96 || a->D == 64) && a->block_q == kPPBM && !force_pp && src32 &&
-                  (a->n_q == 0 || (p.R >= 255 && p.C >= 64))) ? 1 : 0;
+  // Its lane copy offsets are 24-bit products (row x row stride in bytes).
+  const bool str24 = fits24(a->k_str[1]) && fits24(a->v_str[1]) &&
+                     (a->n_x == 0 || (fits24(a->kx_str[1]) && fits24(a->vx_str[1])));
+  // Its loop masks "two-part" descriptors only.  A short last key block of
+  // the frame source that crosses a frame boundary (a source starting
+  // mid-frame, as on a context-parallel shard) has three parts (two frames
+  // and the rows past the end) and is planned "generic".
+  const bool tail_cross = stream_tail_crosses_frame(a->n_q, a->n_k, a->k_tok0, p.C);
+  const bool stream_src = src32 && str24 && !tail_cross;
+  p.use_stream = (!fp32 && (a->D == 128 || a->D == 96 || a->D == 64) && a->block_q == kPPBM && !force_pp &&
+                  stream_src && (a->n_q == 0 || (p.R >= 255 && p.C >= 64))) ? 1 : 0;
   // D = 192 and 256: the wide single-stream loop on the 4-wave kernel's
   // 128-row tiles, which touch at most two query frames when frames have
   // >= 127 rows.
-  if (!fp32 && (a->D == 192 || a->D == 256) && a->block_q == kBM && !force_pp && src32 &&
+  if (!fp32 && (a->D == 192 || a->D == 256) && a->block_q == kBM && !force_pp && stream_src &&
       (a->n_q == 0 || (p.R >= 127 && p.C >= 64)))
     p.use_stream = 1;
   if (a->block_q == kStream12BM) {
     LVSA_REQUIRE(src32, LVSA_ERR_UNSUPPORTED,
-                 "lvsa_attn_fwd: 384-row tiles address each key source with 32-bit byte offsets (source too large)");
+                 "lvsa_attn_fwd: 384-row tiles address each key source with 32-bit byte offsets (source too large); "
+                 "build the plan with block_q 256");
+    LVSA_REQUIRE(!tail_cross, LVSA_ERR_UNSUPPORTED,
+                 "lvsa_attn_fwd: 384-row tiles need the last key block of the frame source inside one frame "
+                 "(n_k %lld, k_tok0 %lld, C %d); build the plan with block_q 256",
+                 (long long)a->n_k, (long long)a->k_tok0, p.C);
     p.use_stream = 1;
   }
   // With a workspace, the single-stream kernel runs one persistent
@@ -335,25 +337,4 @@ extern "C" int lvsa_attn_workspace_query(const lvsa_attn_args* a, int64_t* bytes
                "lvsa_attn_workspace_query: head_dim %d not supported", a->D);
   *bytes = ws_bytes(a);
   return LVSA_OK;
-}
-
-extern "C" int lvsa_attn_fwd_noalloc(const lvsa_attn_args* a, hipStream_t stream) {
-  clear_error();
-  LVSA_REQUIRE(a != nullptr, LVSA_ERR_INVALID_ARG, "lvsa_attn_fwd_noalloc: null args");
-  int64_t need = 0;
-  int rc = lvsa_attn_workspace_query(a, &need);
-  if (rc != LVSA_OK) return rc;
-  LVSA_REQUIRE(need <= (int64_t)LVSA_NOALLOC_SCRATCH_BYTES, LVSA_ERR_CAPACITY,
-               "lvsa_attn_fwd_noalloc: the text-tile split needs %lld bytes of scratch, more than the static "
-               "%lld (LVSA_NOALLOC_SCRATCH_BYTES); call lvsa_attn_fwd with a workspace instead",
-               (long long)need, (long long)LVSA_NOALLOC_SCRATCH_BYTES);
-  lvsa_attn_args b = *a;
-  b.workspace = nullptr;
-  b.workspace_bytes = 0;
-  if (need > 0) {
-    rc = scratch_of_current_device(&b.workspace);
-    if (rc != LVSA_OK) return rc;
-    b.workspace_bytes = LVSA_NOALLOC_SCRATCH_BYTES;
-  }
-  return lvsa_attn_fwd(&b, stream);
 }

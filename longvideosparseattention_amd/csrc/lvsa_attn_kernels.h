@@ -937,10 +937,12 @@ __global__ __launch_bounds__(kPPThreads, 1) void attn_fwd_pp_kernel(AttnParams p
   // uniform 4*ii*RPI rows as the buffer soffset.
   const uint32_t dma_row = (uint32_t)(dw * RPI + lane / NCH);  // row of instruction 0
   const uint32_t dma_c16 = (uint32_t)(((lane % NCH) ^ swz<D>((int)(dma_row & 15))) * 16);
-  // D = 96: a lane whose chunk lies past the row's data reads from an offset
-  // beyond every buffer resource's range, so its copy writes zeros to LDS and
-  // touches no memory.  Row strides are below 16 MiB, so with the soffset of
-  // at most 60 rows the sum stays below 2^32.
+  // D = 96: a lane whose chunk lies past the row's data copies from offset
+  // 0x7FFF0000 plus the soffset: past the buffer resource's range for a
+  // source below that size (zeros, no memory access), else bytes of the
+  // source.  Either way no LDS read touches those chunks.  Row strides are
+  // below 16 MiB, so with the soffset of at most 60 rows the sum stays below
+  // 2^32.
   auto lane_off = [&](uint32_t row_stride) __attribute__((always_inline)) {
     if constexpr (NCV < NCH) {
       if (dma_c16 >= (uint32_t)(16 * NCV)) return 0x7FFF0000u;

@@ -29,19 +29,35 @@ def kernel_head_dim(head_dim: int) -> int:
     return head_dim
 
 
+def stream_tail_crosses_frame(n_q: int, n_k: int, k_tok0: int, key_rows: int) -> bool:
+    """Whether the short last key block of a frame-structured source of ``n_k``
+    rows starting at token ``k_tok0`` crosses a frame boundary (frames of
+    ``key_rows`` tokens).  The plan builder describes such a block as
+    "generic", which the single-stream kernels do not handle; the C entry
+    point makes the same test (``stream_tail_crosses_frame``)."""
+    B = capi.ATTN_BLOCK_K
+    if n_q == 0 or n_k <= 0 or key_rows <= 0:
+        return False
+    t = n_k - B * ((n_k - 1) // B)
+    e = (k_tok0 + n_k) % key_rows
+    return t < B and 0 < e < t
+
+
 def attn_block_q(head_dim: int = 128, dtype: Optional[torch.dtype] = None, frame_rows: int = 0,
-                 key_rows: int = 0) -> int:
+                 key_rows: int = 0, n_k: int = 0, k_tok0: int = 0) -> int:
     """Query rows per attention tile, i.e. which kernel a plan is built for.
 
     384 for head size 64 in 16-bit when query frames span at least 383 rows
-    and key frames at least 64 (``frame_rows``, ``key_rows``): the 12-wave
-    single-stream kernel, three waves per SIMD.  256 for head sizes 64, 96
-    and 128 otherwise: the 8-wave kernels (bf16 / fp16).  128 for 192 and 256:
-    the single-stream kernel's wide map (4 waves, one per SIMD, when query
-    frames span at least 127 rows and key frames at least 64) or else the
-    4-wave kernel, and for fp32 inputs at every head size (the fp32 kernel).
-    ``LVSA_ATTN_BLOCK_Q`` (128, 256 or 384) overrides the choice for 64 and 128
-    in 16-bit (384: head size 64 only); 96 runs on the 8-wave kernel only."""
+    and key frames at least 64 (``frame_rows``, ``key_rows``), and the short
+    last block of a key source of ``n_k`` rows from token ``k_tok0`` lies in
+    one frame: the 12-wave single-stream kernel, three waves per SIMD.  256
+    for head sizes 64, 96 and 128 otherwise: the 8-wave kernels (bf16 /
+    fp16).  128 for 192 and 256: the single-stream kernel's wide map (4
+    waves, one per SIMD, when query frames span at least 127 rows and key
+    frames at least 64) or else the 4-wave kernel, and for fp32 inputs at
+    every head size (the fp32 kernel).  ``LVSA_ATTN_BLOCK_Q`` (128, 256 or
+    384) overrides the choice for 64 and 128 in 16-bit (384: head size 64
+    only); 96 runs on the 8-wave kernel only."""
     kd = kernel_head_dim(head_dim)
     if dtype == torch.float32:
         return 128
@@ -52,9 +68,24 @@ def attn_block_q(head_dim: int = 128, dtype: Optional[torch.dtype] = None, frame
     env = os.environ.get("LVSA_ATTN_BLOCK_Q")
     if env:
         return int(env)
-    if kd == 64 and frame_rows >= 383 and key_rows >= capi.ATTN_BLOCK_K:
+    if (kd == 64 and frame_rows >= 383 and key_rows >= capi.ATTN_BLOCK_K and
+            not stream_tail_crosses_frame(1, n_k, k_tok0, key_rows)):
         return 384
     return 256
+
+
+def stream12_sources_ok(*srcs: Optional[torch.Tensor]) -> bool:
+    """Whether the 12-wave kernel (384-row tiles) can address these key /
+    value sources: its copies use one buffer resource per source with 32-bit
+    byte offsets, and 24-bit lane offsets (row x row stride in bytes).  The C
+    entry point rejects a 384-row plan otherwise."""
+    for t in srcs:
+        if t is None or t.shape[1] == 0:
+            continue
+        row = t.stride(1) * t.element_size()
+        if (t.shape[1] + capi.ATTN_BLOCK_K) * row >= (1 << 32) or row >= (1 << 24):
+            return False
+    return True
 
 
 def _stream(device: torch.device) -> int:
@@ -184,7 +215,10 @@ class BlockPlan:
     n_video_tiles: int
     params: capi.PlanParams
     rel: Optional[torch.Tensor]  # keeps the relation bitmap alive
+    max_row_frames: int = 0
     _verified: bool = False
+    _fallback: Optional["BlockPlan"] = None
+    _fallback_ready: Optional[torch.cuda.Event] = None
 
     @property
     def block_q(self) -> int:
@@ -193,6 +227,30 @@ class BlockPlan:
     @property
     def block_k(self) -> int:
         return self.params.block_k
+
+    def with_block_q_256(self) -> "BlockPlan":
+        """The same relation planned for 256-row tiles (built once, on the
+        current stream): what a 384-row plan falls back to when a call's key
+        sources exceed the 12-wave kernel's addressing."""
+        if self.block_q == 256:
+            return self
+        dev = self.tile_indptr.device
+        capturing = torch.cuda.is_current_stream_capturing()
+        if self._fallback is None:
+            p = self.params
+            self._fallback = plan_build(
+                self.rel, n_q=p.n_q, n_k=p.n_k, n_x=p.n_x, n_tq=p.n_tq, R=p.R, Cf=p.C, q_tok0=p.q_tok0,
+                k_tok0=p.k_tok0, q_frame0=p.q_frame0, max_row_frames=self.max_row_frames, block_q=256,
+                block_k=p.block_k, device=dev)
+            if not capturing:
+                self._fallback_ready = torch.cuda.Event()
+                self._fallback_ready.record(torch.cuda.current_stream(dev))
+        elif self._fallback_ready is not None and not capturing:
+            s = torch.cuda.current_stream(dev)   # a plan shared between streams: order after its build
+            s.wait_event(self._fallback_ready)
+            for t in (self._fallback.tile_indptr, self._fallback.entries, self._fallback.status):
+                t.record_stream(s)
+        return self._fallback
 
     def verify(self) -> None:
         """Raise if the plan overflowed its entry capacity (``status[0]``).
@@ -247,7 +305,7 @@ def plan_build(rel: Optional[torch.Tensor], *, n_q: int, n_k: int, n_x: int = 0,
         capi.check("lvsa_plan_build", capi.lib().lvsa_plan_build(
             C.byref(p), indptr.data_ptr(), entries.data_ptr(), sz.max_entries,
             status.data_ptr(), status.numel() * 4, _stream(device)))
-    return BlockPlan(indptr, entries, status, sz.n_tiles, sz.n_video_tiles, p, rel)
+    return BlockPlan(indptr, entries, status, sz.n_tiles, sz.n_video_tiles, p, rel, max_row_frames)
 
 
 # ─────────────────────────── attention forward ─────────────────────────────
@@ -318,6 +376,8 @@ def attn_args(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, plan: BlockPlan
         n_tq = qt.shape[1]
     else:
         qt = None
+    if plan.block_q == 384 and not stream12_sources_ok(k, v, kx, vx):
+        plan = plan.with_block_q_256()
     pp = plan.params
     if plan.block_k != capi.ATTN_BLOCK_K:
         raise ValueError(f"plan built with block_k={plan.block_k}; the attention kernels walk key blocks of "

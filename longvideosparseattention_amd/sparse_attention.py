@@ -202,8 +202,55 @@ def print_attention_mask_compact(
 
 @dataclass
 class _DeviceState:
+    """The device mask and block plans of one pattern on one GPU.
+
+    A pattern is shared (``LVSAMetadata.build`` returns one instance per set of
+    arguments), so its tensors can be built on one stream and read on others.
+    Every build records ``ready`` on its stream and bumps ``version``; a stream
+    that has not joined the current version first waits for ``ready`` and
+    registers itself with the caching allocator (``record_stream``), so an
+    evicted pattern's memory is not reused while that stream may still read
+    it.  Not done under stream capture: build a pattern before capturing it.
+    """
+
     mask: hip_ops.DeviceMask
     plans: Dict[Tuple, hip_ops.BlockPlan] = field(default_factory=dict)
+    ready: Optional[torch.cuda.Event] = None
+    version: int = 0
+    joined: Dict[int, int] = field(default_factory=dict)   # stream handle -> version it has waited for
+
+    def _tensors(self):
+        m = self.mask
+        ts = [m.frame_indptr, m.frame_indices, m.compact_frames, m.global_frames, m.window_bounds, m.rel_full,
+              m.rel_window, m.info]
+        for p in self.plans.values():
+            ts += [p.tile_indptr, p.entries, p.status]
+            if p._fallback is not None:
+                ts += [p._fallback.tile_indptr, p._fallback.entries, p._fallback.status]
+        return ts
+
+    def built(self, device: torch.device) -> None:
+        """Mark a build just enqueued on the current stream of ``device``."""
+        if torch.cuda.is_current_stream_capturing():
+            return
+        s = torch.cuda.current_stream(device)
+        if self.ready is None:
+            self.ready = torch.cuda.Event()
+        self.ready.record(s)
+        self.version += 1
+        self.joined[s.cuda_stream] = self.version
+
+    def join(self, device: torch.device) -> None:
+        """Order the current stream of ``device`` after every build so far."""
+        if self.ready is None or torch.cuda.is_current_stream_capturing():
+            return
+        s = torch.cuda.current_stream(device)
+        if self.joined.get(s.cuda_stream, 0) == self.version:
+            return
+        s.wait_event(self.ready)
+        for t in self._tensors():
+            t.record_stream(s)
+        self.joined[s.cuda_stream] = self.version
 
 
 # Patterns built by LVSAMetadata.build, shared by every caller that asks for
@@ -463,7 +510,9 @@ class LVSAMetadata:
         st = self._device_state.get(key)
         if st is None:
             st = _DeviceState(hip_ops.mask_build(self._mask_params(), device))
+            st.built(device)
             self._device_state[key] = st
+        st.join(device)
         return st
 
     def ensure_device(self, device: torch.device) -> None:
@@ -499,7 +548,8 @@ class LVSAMetadata:
         """Plan for ``lvsa_sdpa`` semantics: every query row attends all extra
         rows (``k_global``) plus the non-global window frames of its frame."""
         st = self.device_state(device)
-        block_q = hip_ops.attn_block_q(head_dim, dtype, self.num_patches, self.num_patches)
+        block_q = hip_ops.attn_block_q(head_dim, dtype, self.num_patches, self.num_patches, n_k=n_k,
+                                       k_tok0=self.global_token_start)
         key = ("window", n_q, n_k, n_extra, block_q)
         plan = st.plans.get(key)
         if plan is None:
@@ -508,6 +558,7 @@ class LVSAMetadata:
                 st.mask.rel_window, n_q=n_q, n_k=n_k, n_x=n_extra, R=P, Cf=P, q_tok0=gts, k_tok0=gts,
                 q_frame0=gts // P, max_row_frames=max(1, 2 * self.window_size + 1), block_q=block_q)
             st.plans[key] = plan
+            st.built(st.mask.info.device)
         return plan
 
     def full_plan(self, device: torch.device, n_q: int, n_k: int, n_text_k: int, n_text_q: int,
@@ -517,7 +568,7 @@ class LVSAMetadata:
         if self.world != 1:
             raise NotImplementedError("zero-copy LVSA attention needs the whole sequence on one GPU (world=1)")
         st = self.device_state(device)
-        block_q = hip_ops.attn_block_q(head_dim, dtype, self.num_patches, self.num_patches)
+        block_q = hip_ops.attn_block_q(head_dim, dtype, self.num_patches, self.num_patches, n_k=n_k)
         key = ("full", n_q, n_k, n_text_k, n_text_q, block_q)
         plan = st.plans.get(key)
         if plan is None:
@@ -526,6 +577,7 @@ class LVSAMetadata:
                 st.mask.rel_full, n_q=n_q, n_k=n_k, n_x=n_text_k, n_tq=n_text_q, R=P, Cf=P,
                 max_row_frames=max(1, self.max_row_frames), block_q=block_q)
             st.plans[key] = plan
+            st.built(st.mask.info.device)
         return plan
 
 
@@ -606,6 +658,10 @@ def lvsa_flashinfer(
     """
     B = query_padded.shape[0]
     H, D = query_padded.shape[2], query_padded.shape[3]
+    if hasattr(fi_wrapper, "run_batched"):
+        # this package's wrapper: the whole batch in one launch (the reference
+        # runs one FlashInfer call per batch element)
+        return fi_wrapper.run_batched(query_padded, k_compact, v_compact)[:, :local_seq]
     output = query_padded.new_empty(B, fi_M, H, D)
     for b in range(B):
         output[b] = fi_wrapper.run(query_padded[b], k_compact[b], v_compact[b])

@@ -169,11 +169,27 @@ def test_lvsa_sdpa_with_k_global_and_text(gpu):
     _close(fused, ro, "fused vs lvsa_sdpa reference")
 
 
-def test_lvsa_sdpa_context_parallel_shard(gpu):
-    # rank 1 of 2: local queries/keys, globals assembled from the full sequence.
-    T, P, W, H, D, world, rank = 12, 50, 2, 2, 128, 2, 1
+CP_SHARDS = [
+    # T, P, W, kfi, off, H, D, world, rank
+    (12, 50, 2, 5, 3, 2, 128, 2, 1),
+    # P >= 255 (single-stream kernels) with the shard's short last key block
+    # [256, 312) crossing the frame boundary at 260: planned "generic", so
+    # these run the compiler-built kernels
+    (6, 260, 1, 3, 1, 2, 128, 5, 0),
+    (6, 260, 1, 3, 1, 2, 64, 5, 0),
+    (6, 260, 1, 3, 1, 2, 192, 5, 0),
+    # P >= 383 (384-row tiles for head size 64) with a crossing last block:
+    # keys [384, 440), boundary at 385
+    (8, 385, 1, 3, 2, 2, 64, 7, 0),
+]
+
+
+@pytest.mark.parametrize("cfg", CP_SHARDS, ids=[str(c) for c in CP_SHARDS])
+def test_lvsa_sdpa_context_parallel_shard(cfg, gpu):
+    # one rank: local queries/keys, globals assembled from the full sequence.
+    T, P, W, kfi, off, H, D, world, rank = cfg
     guards = lv.compute_boundary_guard_frames(T, T * P // world, P, world, W)
-    m = _meta(T, P, W, 1, 5, 3, rank=rank, world=world, guards=guards)
+    m = _meta(T, P, W, 1, kfi, off, rank=rank, world=world, guards=guards)
     q, k, v = _draw([(1, T * P, H, D)] * 3)
     s, e = m.global_token_start, m.global_token_start + m.local_seq
     kg = torch.cat([k[:, g * P:(g + 1) * P] for g in m.global_indices], 1)
@@ -211,6 +227,37 @@ def test_flashinfer_backend_and_wrapper(gpu):
     _close(out, ro, "flashinfer backend")
     o2, lse2 = w.run(q[0], ck[0], cv[0], return_lse=True)
     torch.testing.assert_close(lse2.cpu(), (rl[0].transpose(0, 1) / math.log(2.0)).cpu(), atol=3e-2, rtol=0)
+
+
+def test_flashinfer_backend_batch_of_two(gpu):
+    """B = 2 (classifier-free guidance): the backend runs the batch in one
+    launch (run_batched), bit for bit what one run() per element gives, and
+    matches the oracle per element."""
+    T, P, W, H, Hkv, D = 9, 96, 1, 4, 2, 128
+    m = _meta(T, P, W, 1, 4, 2)
+    m.ensure_device(gpu)
+    q = _draw([(2, T * P, H, D)], seed=11)[0].to(gpu)
+    k, v = (x.to(gpu) for x in _draw([(2, T * P, Hkv, D)] * 2, seed=12))
+    kg, vg = lv.build_global_kv(k, v, m.global_indices, P)
+    ck = k.new_zeros(2, m.fi_N, Hkv, D)
+    cv = k.new_zeros(2, m.fi_N, Hkv, D)
+    for src, dst in m.fi_global_copies:
+        ck[:, dst:dst + P], cv[:, dst:dst + P] = kg[:, src:src + P], vg[:, src:src + P]
+    for src, dst in m.fi_local_copies:
+        ck[:, dst:dst + P], cv[:, dst:dst + P] = k[:, src:src + P], v[:, src:src + P]
+    w = lv.BlockSparseAttentionWrapper(torch.empty(1, dtype=torch.uint8, device=gpu))
+    w.plan(m.fi_indptr, m.fi_indices, M=m.fi_M, N=m.fi_N, R=P, C=P, num_qo_heads=H, num_kv_heads=Hkv,
+           head_dim=D, q_data_type="bfloat16")
+    qp = q.new_zeros(2, m.fi_M, H, D)
+    qp[:, :m.local_seq] = q
+    out = lv.sparse_windowed_attention(qp, k, v, kg, vg, m, backend="flashinfer", k_compact=ck, v_compact=cv,
+                                       fi_wrapper=w)
+    assert out.shape == (2, m.local_seq, H, D)
+    rows = [set(r) for r in om.build_frame_mask(T, P, W, 1, 4, offset=2).rows]
+    for b in range(2):
+        assert torch.equal(out[b], w.run(qp[b], ck[b], cv[b])[:m.local_seq])
+        ro, _ = oa.per_frame_sdpa(q[b:b + 1].float(), k[b:b + 1].float(), v[b:b + 1].float(), rows, P)
+        _close(out[b:b + 1], ro, f"flashinfer backend batch element {b}")
 
 
 def test_dual_stream_runner_gqa(gpu):
@@ -511,21 +558,24 @@ def test_baseline_sweep_spot_frames(cfg, gpu):
 
 
 ALL_FRAMES = [
-    # name, T, P, W, kfi, off, H, D, n_txt[, dtype[, Hkv]] (full BASELINE sizes, bf16 and Hkv = H unless
-    # given, one offset each)
-    ("wan4x_off3", 84, 1560, 2, 8, 3, 12, 128, 0),
-    ("wan6x_w2_off4", 121, 1560, 2, 8, 4, 12, 128, 0),
-    ("hv_off5", 49, 1590, 2, 8, 5, 16, 128, 256),
-    ("cog_off1", 13, 1350, 1, 4, 1, 48, 64, 226),
+    # name, T, P, W, kfi, offsets, H, D, n_txt[, dtype[, Hkv]] (full BASELINE sizes, bf16 and Hkv = H
+    # unless given).  Wan 4x, HunyuanVideo and CogVideoX at every keyframe rotation; the Wan 6x window
+    # sweep (+-1, +-2, +-4) at one rotation each.
+    ("wan4x_all_offsets", 84, 1560, 2, 8, tuple(range(8)), 12, 128, 0),
+    ("wan6x_w1_off3", 121, 1560, 1, 8, (3,), 12, 128, 0),
+    ("wan6x_w2_off4", 121, 1560, 2, 8, (4,), 12, 128, 0),
+    ("wan6x_w4_off6", 121, 1560, 4, 8, (6,), 12, 128, 0),
+    ("hv_all_offsets", 49, 1590, 2, 8, tuple(range(8)), 16, 128, 256),
+    ("cog_all_offsets", 13, 1350, 1, 4, tuple(range(4)), 48, 64, 226),
     # the plugin's other head sizes at the Wan 4x geometry (96: D = 128 LDS layout; 192, 256: wide map)
-    ("wan4x_d96_off6", 84, 1560, 2, 8, 6, 12, 96, 0),
-    ("wan4x_d192_off1", 84, 1560, 2, 8, 1, 12, 192, 0),
-    ("wan4x_d256_off7", 84, 1560, 2, 8, 7, 12, 256, 0),
+    ("wan4x_d96_off6", 84, 1560, 2, 8, (6,), 12, 96, 0),
+    ("wan4x_d192_off1", 84, 1560, 2, 8, (1,), 12, 192, 0),
+    ("wan4x_d256_off7", 84, 1560, 2, 8, (7,), 12, 256, 0),
     # fp16 inputs (the loops' f16 variants)
-    ("wan4x_f16_off0", 84, 1560, 2, 8, 0, 12, 128, 0, torch.float16),
-    ("cog_f16_off2", 13, 1350, 1, 4, 2, 48, 64, 226, torch.float16),
+    ("wan4x_f16_off0", 84, 1560, 2, 8, (0,), 12, 128, 0, torch.float16),
+    ("cog_f16_off2", 13, 1350, 1, 4, (2,), 48, 64, 226, torch.float16),
     # grouped K/V heads (3 query heads per K/V head), read in place
-    ("wan4x_gqa3_off2", 84, 1560, 2, 8, 2, 12, 128, 0, torch.bfloat16, 4),
+    ("wan4x_gqa3_off2", 84, 1560, 2, 8, (2,), 12, 128, 0, torch.bfloat16, 4),
 ]
 
 
@@ -533,8 +583,9 @@ ALL_FRAMES = [
 def test_baseline_all_frames(cfg, gpu):
     """Every query frame (not a sample) at full size against the fp32 oracle
     (its per-frame gather and dense attention run on the GPU in fp32), with
-    the LSE; text rows too."""
-    name, T, P, W, kfi, off, H, D, n_txt = cfg[:9]
+    the LSE; text rows too.  Each listed keyframe rotation rebuilds the
+    pattern (lvsa/lvsa_processor.py:317-331) on the same inputs."""
+    name, T, P, W, kfi, offsets, H, D, n_txt = cfg[:9]
     dt = cfg[9] if len(cfg) > 9 else torch.bfloat16
     Hkv = cfg[10] if len(cfg) > 10 else H
     N = T * P
@@ -543,19 +594,23 @@ def test_baseline_all_frames(cfg, gpu):
     k, v = (torch.randn(1, N, Hkv, D, generator=g, device=gpu).to(dt) for _ in range(2))
     qt = torch.randn(1, n_txt, H, D, generator=g, device=gpu).to(dt)
     kt, vt = (torch.randn(1, n_txt, Hkv, D, generator=g, device=gpu).to(dt) for _ in range(2))
-    m = _meta(T, P, W, 1, kfi, off)
     args = dict(k_text=kt, v_text=vt, q_text=qt) if n_txt else {}
-    res = lv.lvsa_attention(q, k, v, m, return_lse=True, **args)
-    o, lse = (res[0], res[2]) if n_txt else res
-    rows = [set(r) for r in om.build_frame_mask(T, P, W, 1, kfi, offset=off).rows]
-    ro, rl = oa.per_frame_sdpa(q.float(), k.float(), v.float(), rows, P, k_extra=kt.float() if n_txt else None,
-                               v_extra=vt.float() if n_txt else None)
-    assert not torch.isnan(ro).any()
-    _close(o, ro, name)
-    torch.testing.assert_close(lse.float(), rl, atol=2e-2, rtol=0, msg=name)
-    if n_txt:
-        rto, _ = oa.text_row_attention(qt.float(), k.float(), v.float(), kt.float(), vt.float())
-        _close(res[1], rto, name + " text rows")
+    for off in offsets:
+        tag = f"{name} offset {off}"
+        print(f"  {tag}", flush=True)
+        m = _meta(T, P, W, 1, kfi, off)
+        res = lv.lvsa_attention(q, k, v, m, return_lse=True, **args)
+        o, lse = (res[0], res[2]) if n_txt else res
+        rows = [set(r) for r in om.build_frame_mask(T, P, W, 1, kfi, offset=off).rows]
+        ro, rl = oa.per_frame_sdpa(q.float(), k.float(), v.float(), rows, P,
+                                   k_extra=kt.float() if n_txt else None, v_extra=vt.float() if n_txt else None)
+        assert not torch.isnan(ro).any()
+        _close(o, ro, tag)
+        torch.testing.assert_close(lse.float(), rl, atol=2e-2, rtol=0, msg=tag)
+        del ro, rl
+        if n_txt and off == offsets[0]:
+            rto, _ = oa.text_row_attention(qt.float(), k.float(), v.float(), kt.float(), vt.float())
+            _close(res[1], rto, tag + " text rows")
 
 
 SUPPORT = [
@@ -819,3 +874,27 @@ def test_stream_kernel_random_geometries(seed, D, gpu, monkeypatch):
     if n_txt:
         rto, _ = oa.text_row_attention(qt.float(), k.float(), v.float(), kt.float(), vt.float())
         _close(res[1], rto, what + " text rows")
+
+
+def test_shared_pattern_across_streams(gpu):
+    """LVSAMetadata.build shares one pattern per set of arguments: built (mask
+    and plan) on one stream and then used on another, the second stream waits
+    for the build and registers itself with the allocator, and both give the
+    same output bit for bit."""
+    T, P, W, kfi, off, H, D = 11, 264, 1, 4, 2, 2, 128
+    m = _meta(T, P, W, 1, kfi, off)
+    q, k, v = (x.to(gpu) for x in _draw([(1, T * P, H, D)] * 3, seed=5))
+    s1, s2 = torch.cuda.Stream(gpu), torch.cuda.Stream(gpu)
+    s1.wait_stream(torch.cuda.current_stream(gpu))
+    s2.wait_stream(torch.cuda.current_stream(gpu))
+    with torch.cuda.stream(s1):
+        o1 = lv.lvsa_attention(q, k, v, m)
+    with torch.cuda.stream(s2):
+        o2 = lv.lvsa_attention(q, k, v, m)
+    torch.cuda.synchronize(gpu)
+    st = m.device_state(gpu)
+    assert st.joined.get(s1.cuda_stream) == st.version and st.joined.get(s2.cuda_stream) == st.version
+    assert torch.equal(o1, o2)
+    rows = [set(r) for r in om.build_frame_mask(T, P, W, 1, kfi, offset=off).rows]
+    ro, _ = oa.per_frame_sdpa(q.float(), k.float(), v.float(), rows, P)
+    _close(o2, ro, "second stream")

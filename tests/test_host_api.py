@@ -157,8 +157,40 @@ def test_head_sizes_of_the_plugin():
     assert hip_ops.attn_block_q(64, torch.bfloat16, 1350, 63) == 256
     assert hip_ops.attn_block_q(64, torch.float32, 1350, 1350) == 128
     assert hip_ops.attn_block_q(128, torch.bfloat16, 1560, 1560) == 256
+    # a shard whose short last key block crosses a frame boundary: 256-row tiles
+    assert hip_ops.attn_block_q(64, torch.bfloat16, 385, 385, n_k=440, k_tok0=0) == 256
+    assert hip_ops.attn_block_q(64, torch.bfloat16, 385, 385, n_k=440, k_tok0=440) == 384
     with pytest.raises(ValueError, match="head_dim 80"):
         hip_ops.kernel_head_dim(80)
+
+
+def _frame_parts_of_last_block(n_k, k_tok0, C, block=64):
+    """Parts of the last key block as the plan builder counts them
+    (lvsa_mask.hip frame_desc): the key frames its rows fall in, plus one for
+    the rows past the end of the source when the block is short."""
+    k0 = block * ((n_k - 1) // block)
+    frames = {(k_tok0 + k) // C for k in range(k0, n_k)}
+    return len(frames) + (1 if n_k - k0 < block else 0)
+
+
+def test_stream_tail_test_matches_the_plan_descriptor():
+    """stream_tail_crosses_frame (mirrored by the C entry point's gate of the
+    single-stream kernels) is true exactly when the plan builder would make
+    the source's last key block a three-part ("generic") descriptor."""
+    import random
+
+    from longvideosparseattention_amd import hip_ops
+
+    rng = random.Random(7)
+    cases = [(312, 0, 260), (440, 0, 385), (440, 440, 385), (64, 30, 64), (1, 5, 64), (320, 0, 260)]
+    cases += [(rng.randint(1, 3000), rng.randint(0, 5000), rng.randint(64, 700)) for _ in range(3000)]
+    hits = 0
+    for n_k, k_tok0, C in cases:
+        want = _frame_parts_of_last_block(n_k, k_tok0, C) >= 3
+        assert hip_ops.stream_tail_crosses_frame(1, n_k, k_tok0, C) == want, (n_k, k_tok0, C)
+        hits += want
+    assert hits > 20
+    assert not hip_ops.stream_tail_crosses_frame(0, 312, 0, 260)   # no video queries: no frame plan
 
 
 def test_query_length_must_match_metadata():
@@ -244,3 +276,21 @@ def test_build_returns_one_shared_pattern_per_argument_set(monkeypatch):
     x, y = (lv.LVSAMetadata.build(keyframe_offset=1, **kw) for _ in range(2))
     assert x is not y and x.global_indices == y.global_indices
     sa.clear_metadata_cache()
+
+
+def test_stream12_source_limits():
+    """384-row plans fall back to 256-row tiles (hip_ops.attn_args) for key
+    sources the 12-wave kernel cannot address: 32-bit byte offsets per source
+    and 24-bit lane offsets (row stride in bytes below 16 MiB)."""
+    from longvideosparseattention_amd import hip_ops
+
+    def src(rows, row_stride):
+        return torch.empty_strided((1, rows, 1, 64), (0, row_stride, 64, 1), dtype=torch.bfloat16, device="meta")
+
+    assert hip_ops.stream12_sources_ok(src(1000, 3072), src(1000, 3072), None, None)
+    assert not hip_ops.stream12_sources_ok(src(1000, 8 << 20), src(1000, 64))        # 16 MiB row stride
+    assert hip_ops.stream12_sources_ok(src(100, (8 << 20) - 8))                       # just below both limits
+    big = (1 << 31) // 3072                                                          # rows of 6 KiB
+    assert not hip_ops.stream12_sources_ok(src(big - 63, 3072))                      # (rows + 64) * 6 KiB >= 2^32
+    assert hip_ops.stream12_sources_ok(src(big - 65, 3072))
+    assert hip_ops.stream12_sources_ok(src(0, 8 << 20))                              # empty source: nothing read
