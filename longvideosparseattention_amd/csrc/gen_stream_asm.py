@@ -801,8 +801,11 @@ def operands(D: int, nw: int = 8, rs: bool = False) -> list[str]:
 # sub-iteration (1.2% / 1.4% faster than 3 and 2; lookahead 2 and 5, start 3
 # and no mid-block entry load measured slower); at D = 256 its copies go out
 # every third MFMA (1.0% faster than every second; at D = 192, whose blocks
-# have 48 MFMAs, 8% slower; every MFMA 3-5% slower).  Measured
-# neutral and not used: the D = 64 softmax spread over one more MFMA slot
+# have 48 MFMAs, 8% slower; every MFMA 3-5% slower), and waits for LDS
+# operands once per two MFMAs (its one wave per SIMD issues every
+# instruction of the loop itself: D = 192 0.9% fewer cycles and 0.4% less
+# time over three pairs, D = 256 0.3% fewer cycles; D = 96 2% more cycles).
+# Measured neutral and not used: the D = 64 softmax spread over one more MFMA slot
 # (sm_start 1), one LDS wait per two MFMAs (wait_pair), 8 wait states before
 # the row sum is read (tail_nop 8), QK / PV MFMAs in pairs or grouped
 # (mfma_order).
@@ -812,9 +815,9 @@ PRODUCT = {128: dict(lead=2, early_load=True, dot_init=True, and_scc=True, copy_
                     tail_split=True, mask_fast=True),
            64: dict(dot_init=True, and_scc=True, copy_split=True, rs_mfma=True, tail_split=True, mask_fast=True),
            256: dict(early_load=True, dot_init=True, and_scc=True, copy_split=True, rs_mfma=True, tail_split=True,
-                     mask_fast=True, la=4, sm_start=4, copy_every=3),
+                     mask_fast=True, la=4, sm_start=4, copy_every=3, wait_pair=True),
            192: dict(early_load=True, dot_init=True, and_scc=True, copy_split=True, rs_mfma=True, tail_split=True,
-                     mask_fast=True, la=4, sm_start=4)}
+                     mask_fast=True, la=4, sm_start=4, wait_pair=True)}
 
 
 def render(per_d: dict | None = None, **opts) -> str:
@@ -825,7 +828,7 @@ def render(per_d: dict | None = None, **opts) -> str:
     for D, nw in ((128, 8), (96, 8), (64, 8), (64, 12), (256, 4), (192, 4)):
         pf = prefix(D, nw)
         for dt, name in (("bf16", f"{pf}_LOOP_BF16"), ("f16", f"{pf}_LOOP_F16")):
-            o = {**PRODUCT[D], **opts, **(per_d or {}).get(D, {})}
+            o = {**PRODUCT[D], **opts, **(per_d or {}).get(D, {}), **(per_d or {}).get((D, nw), {})}
             lines = Gen(dt, D=D, nw=nw, **o).build()
             out.append(f"#define {name} \\")
             for ln in lines:

@@ -559,12 +559,12 @@ def test_baseline_sweep_spot_frames(cfg, gpu):
 
 ALL_FRAMES = [
     # name, T, P, W, kfi, offsets, H, D, n_txt[, dtype[, Hkv]] (full BASELINE sizes, bf16 and Hkv = H
-    # unless given).  Wan 4x, HunyuanVideo and CogVideoX at every keyframe rotation; the Wan 6x window
-    # sweep (+-1, +-2, +-4) at one rotation each.
+    # unless given).  Wan 4x, Wan 6x (window +-2), HunyuanVideo and CogVideoX at every keyframe
+    # rotation; the Wan 6x window sweep points +-1 and +-4 at four rotations each.
     ("wan4x_all_offsets", 84, 1560, 2, 8, tuple(range(8)), 12, 128, 0),
-    ("wan6x_w1_off3", 121, 1560, 1, 8, (3,), 12, 128, 0),
-    ("wan6x_w2_off4", 121, 1560, 2, 8, (4,), 12, 128, 0),
-    ("wan6x_w4_off6", 121, 1560, 4, 8, (6,), 12, 128, 0),
+    ("wan6x_w1_four_offsets", 121, 1560, 1, 8, (0, 3, 5, 7), 12, 128, 0),
+    ("wan6x_w2_all_offsets", 121, 1560, 2, 8, tuple(range(8)), 12, 128, 0),
+    ("wan6x_w4_four_offsets", 121, 1560, 4, 8, (1, 2, 6, 7), 12, 128, 0),
     ("hv_all_offsets", 49, 1590, 2, 8, tuple(range(8)), 16, 128, 256),
     ("cog_all_offsets", 13, 1350, 1, 4, tuple(range(4)), 48, 64, 226),
     # the plugin's other head sizes at the Wan 4x geometry (96: D = 128 LDS layout; 192, 256: wide map)
