@@ -189,3 +189,23 @@ def test_plan_rejects_query_rows_outside_relation():
     assert b"relation rows [0, 9]" in lib.lvsa_last_error()
     p.rel_rows = 10
     assert lib.lvsa_plan_sizes_query(C.byref(p), 5, C.byref(s)) == 0
+
+
+def test_attn_rejects_384_row_plans_the_12_wave_kernel_cannot_run():
+    """384-row tiles run only on the 12-wave single-stream kernel, whose loop
+    masks "two-part" descriptors and addresses each key source with 32-bit
+    byte offsets: a frame source whose short last key block crosses a frame
+    boundary (keys [384, 440) over frames of 385: planned "generic"), or a
+    source of 2^32 bytes or more, is rejected before anything is launched."""
+    lib = _capi.lib()
+    a = _attn_args(n_q=440, rel_rows=2, n_k=440)
+    a.D, a.block_q, a.R, a.C = 64, 384, 385, 385
+    a.n_video_tiles = a.n_tiles = 2
+    a.q_str = a.o_str = a.k_str = a.v_str = _capi._Str3(1 << 20, 64, 64)
+    assert lib.lvsa_attn_fwd(C.byref(a), None) == -2
+    assert b"last key block of the frame source inside one frame" in lib.lvsa_last_error()
+    a.k_tok0 = 440                                   # keys [440, 880): boundary 770 outside the tail
+    a.k_str = _capi._Str3(1 << 40, 1 << 23, 64)      # 16 MiB rows: 2^32 bytes well before the end
+    assert lib.lvsa_attn_fwd(C.byref(a), None) == -2
+    err = lib.lvsa_last_error()
+    assert b"16 MiB" in err or b"32-bit byte offsets" in err
