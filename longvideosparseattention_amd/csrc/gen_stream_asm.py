@@ -808,16 +808,24 @@ def operands(D: int, nw: int = 8, rs: bool = False) -> list[str]:
 # Measured neutral and not used: the D = 64 softmax spread over one more MFMA slot
 # (sm_start 1), one LDS wait per two MFMAs (wait_pair), 8 wait states before
 # the row sum is read (tail_nop 8), QK / PV MFMAs in pairs or grouped
-# (mfma_order).
+# (mfma_order).  Measured in cycles (GRBM_GUI_ACTIVE) and time, paired on one
+# box: D = 96 with the softmax one slot earlier and 10 wait states before the
+# row sum is read, 3.5% fewer cycles and 1.0% less time; the 12-wave D = 64
+# loop with the same start and 8 wait states, 2.8% / 1.2%; D = 128 with 8 or
+# 10 wait states, 1% more cycles (it keeps 12), D = 256 with 8, 0.6% more.
 PRODUCT = {128: dict(lead=2, early_load=True, dot_init=True, and_scc=True, copy_split=True, rs_mfma=True,
                      tail_split=True, mask_fast=True),
            96: dict(lead=2, early_load=True, dot_init=True, and_scc=True, copy_split=True, rs_mfma=True,
-                    tail_split=True, mask_fast=True),
+                    tail_split=True, mask_fast=True, sm_start=1, tail_nop=10),
            64: dict(dot_init=True, and_scc=True, copy_split=True, rs_mfma=True, tail_split=True, mask_fast=True),
            256: dict(early_load=True, dot_init=True, and_scc=True, copy_split=True, rs_mfma=True, tail_split=True,
                      mask_fast=True, la=4, sm_start=4, copy_every=3, wait_pair=True),
            192: dict(early_load=True, dot_init=True, and_scc=True, copy_split=True, rs_mfma=True, tail_split=True,
                      mask_fast=True, la=4, sm_start=4, wait_pair=True)}
+# Options of one map only, over PRODUCT[D]: the 12-wave D = 64 loop starts
+# its softmax one MFMA slot earlier and reads the row sum 8 wait states after
+# its MFMA (the compiler's own count for a 16x16x32 result read by VALU).
+PRODUCT_MAP = {(64, 12): dict(sm_start=1, tail_nop=8)}
 
 
 def render(per_d: dict | None = None, **opts) -> str:
@@ -828,7 +836,8 @@ def render(per_d: dict | None = None, **opts) -> str:
     for D, nw in ((128, 8), (96, 8), (64, 8), (64, 12), (256, 4), (192, 4)):
         pf = prefix(D, nw)
         for dt, name in (("bf16", f"{pf}_LOOP_BF16"), ("f16", f"{pf}_LOOP_F16")):
-            o = {**PRODUCT[D], **opts, **(per_d or {}).get(D, {}), **(per_d or {}).get((D, nw), {})}
+            o = {**PRODUCT[D], **PRODUCT_MAP.get((D, nw), {}), **opts, **(per_d or {}).get(D, {}),
+                 **(per_d or {}).get((D, nw), {})}
             lines = Gen(dt, D=D, nw=nw, **o).build()
             out.append(f"#define {name} \\")
             for ln in lines:
@@ -853,7 +862,7 @@ def census(D: int, nw: int, dt: str = "bf16") -> dict:
     four unrolled blocks between LOOP and its back branch) of the product's
     loop for (D, nw): the common path, without the subroutines a masked
     block or the rare case calls."""
-    lines = Gen(dt, D=D, nw=nw, **PRODUCT[D]).build()
+    lines = Gen(dt, D=D, nw=nw, **{**PRODUCT[D], **PRODUCT_MAP.get((D, nw), {})}).build()
     a = next(i for i, x in enumerate(lines) if x.startswith("LOOP_"))
     b = next(i for i, x in enumerate(lines) if x.startswith("s_branch LOOP_"))
     c = dict.fromkeys(CENSUS_KINDS, 0)
