@@ -812,7 +812,9 @@ def operands(D: int, nw: int = 8, rs: bool = False) -> list[str]:
 # box: D = 96 with the softmax one slot earlier and 10 wait states before the
 # row sum is read, 3.5% fewer cycles and 1.0% less time; the 12-wave D = 64
 # loop with the same start and 8 wait states, 2.8% / 1.2%; D = 128 with 8 or
-# 10 wait states, 1% more cycles (it keeps 12), D = 256 with 8, 0.6% more.
+# 10 wait states, 1% more cycles (it keeps 12), D = 256 with 8, 0.6% more;
+# D = 192 with 8 wait states and its softmax one slot later (five MFMA slots
+# into the sub-iteration), 1.25% fewer cycles and 0.75% less time.
 PRODUCT = {128: dict(lead=2, early_load=True, dot_init=True, and_scc=True, copy_split=True, rs_mfma=True,
                      tail_split=True, mask_fast=True),
            96: dict(lead=2, early_load=True, dot_init=True, and_scc=True, copy_split=True, rs_mfma=True,
@@ -821,7 +823,7 @@ PRODUCT = {128: dict(lead=2, early_load=True, dot_init=True, and_scc=True, copy_
            256: dict(early_load=True, dot_init=True, and_scc=True, copy_split=True, rs_mfma=True, tail_split=True,
                      mask_fast=True, la=4, sm_start=4, copy_every=3, wait_pair=True),
            192: dict(early_load=True, dot_init=True, and_scc=True, copy_split=True, rs_mfma=True, tail_split=True,
-                     mask_fast=True, la=4, sm_start=4, wait_pair=True)}
+                     mask_fast=True, la=4, sm_start=5, wait_pair=True, tail_nop=8)}
 # Options of one map only, over PRODUCT[D]: the 12-wave D = 64 loop starts
 # its softmax one MFMA slot earlier and reads the row sum 8 wait states after
 # its MFMA (the compiler's own count for a 16x16x32 result read by VALU).
