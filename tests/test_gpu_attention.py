@@ -576,6 +576,9 @@ ALL_FRAMES = [
     ("cog_f16_off2", 13, 1350, 1, 4, (2,), 48, 64, 226, torch.float16),
     # grouped K/V heads (3 query heads per K/V head), read in place
     ("wan4x_gqa3_off2", 84, 1560, 2, 8, (2,), 12, 128, 0, torch.bfloat16, 4),
+    # batch of two (classifier-free guidance in the plugin): the batch index is a grid dimension
+    ("cog_b2_off0", 13, 1350, 1, 4, (0,), 48, 64, 226, torch.bfloat16, 48, 2),
+    ("wan4x_b2_off5", 84, 1560, 2, 8, (5,), 12, 128, 0, torch.bfloat16, 12, 2),
 ]
 
 
@@ -588,12 +591,13 @@ def test_baseline_all_frames(cfg, gpu):
     name, T, P, W, kfi, offsets, H, D, n_txt = cfg[:9]
     dt = cfg[9] if len(cfg) > 9 else torch.bfloat16
     Hkv = cfg[10] if len(cfg) > 10 else H
+    B = cfg[11] if len(cfg) > 11 else 1
     N = T * P
     g = torch.Generator(device=gpu).manual_seed(37)
-    q = torch.randn(1, N, H, D, generator=g, device=gpu).to(dt)
-    k, v = (torch.randn(1, N, Hkv, D, generator=g, device=gpu).to(dt) for _ in range(2))
-    qt = torch.randn(1, n_txt, H, D, generator=g, device=gpu).to(dt)
-    kt, vt = (torch.randn(1, n_txt, Hkv, D, generator=g, device=gpu).to(dt) for _ in range(2))
+    q = torch.randn(B, N, H, D, generator=g, device=gpu).to(dt)
+    k, v = (torch.randn(B, N, Hkv, D, generator=g, device=gpu).to(dt) for _ in range(2))
+    qt = torch.randn(B, n_txt, H, D, generator=g, device=gpu).to(dt)
+    kt, vt = (torch.randn(B, n_txt, Hkv, D, generator=g, device=gpu).to(dt) for _ in range(2))
     args = dict(k_text=kt, v_text=vt, q_text=qt) if n_txt else {}
     for off in offsets:
         tag = f"{name} offset {off}"
