@@ -292,14 +292,21 @@ extern "C" int lvsa_attn_fwd(const lvsa_attn_args* a, hipStream_t stream) {
                  (long long)a->n_k, (long long)a->k_tok0, p.C);
     p.use_stream = 1;
   }
+  // D = 64 on 256-row tiles: the dual map (64 rows per wave, 4 waves, two
+  // work-groups per CU); LVSA_D64_WAVES=8 selects 8 waves of 32 rows instead
+  // (comparisons).
+  const char* wenv = getenv("LVSA_D64_WAVES");
+  p.dual = (p.use_stream && a->D == 64 && a->block_q == kPPBM && !(wenv && strcmp(wenv, "8") == 0)) ? 1 : 0;
   // With a workspace, the single-stream kernel runs one persistent
-  // work-group per CU over the work queues (counters zeroed first).
+  // work-group per CU (two with the dual map) over the work queues (counters
+  // zeroed first).
   p.queues = nullptr;
   p.grid = (int)work;
   const int cus = cu_count();
-  if (p.use_stream && a->workspace && cus > 0 && work > cus) {
+  const int per_cu = p.dual ? 2 : 1;
+  if (p.use_stream && a->workspace && cus > 0 && work > per_cu * cus) {
     p.queues = (uint32_t*)((char*)a->workspace + queue_offset(text_ws_bytes(a, chunks)));
-    p.grid = cus;
+    p.grid = per_cu * cus;
     hipLaunchKernelGGL(queue_reset_kernel, dim3(1), dim3(64), 0, stream, p.queues);
     const int qrc = launch_status("lvsa_attn_fwd (queue reset)");
     if (qrc != LVSA_OK) return qrc;

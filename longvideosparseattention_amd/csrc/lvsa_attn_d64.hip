@@ -17,6 +17,16 @@ int launch_d64(const AttnParams& prm, int block_q, bool bf16, hipStream_t stream
     }
     return launch_status("lvsa_attn_fwd");
   }
+  if (block_q == kPPBM && prm.use_stream && prm.dual) {
+    // 4 waves of 64 rows, two work-groups per CU
+    if (bf16) {
+      hipLaunchKernelGGL((attn_fwd_stream_kernel<64, 4, __bf16>), dim3(prm.grid), dim3(64 * 4), 0, stream, prm);
+    } else {
+      hipLaunchKernelGGL((attn_fwd_stream_kernel<64, 4, _Float16>), dim3(prm.grid), dim3(64 * 4), 0, stream,
+                         prm);
+    }
+    return launch_status("lvsa_attn_fwd");
+  }
   if (block_q == kPPBM && prm.use_stream) {
     if (bf16) {
       hipLaunchKernelGGL((attn_fwd_stream_kernel<64, 8, __bf16>), dim3(prm.grid), dim3(kPPThreads), 0, stream, prm);

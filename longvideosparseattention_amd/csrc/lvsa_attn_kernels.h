@@ -75,8 +75,11 @@ struct AttnParams {
   // descriptors "none" and "two-part", which is all such a plan holds when
   // query frames span at least 255 rows and key frames at least 64)
   int use_stream;
+  // D = 64, 256-row tiles on the single-stream kernel: the dual map (4 waves
+  // of 64 rows, two work-groups per CU) rather than 8 waves of 32 rows
+  int dual;
   // Work queues (single-stream kernel with a workspace): `grid` persistent
-  // work-groups, one per CU, take work items from 8 queues, one per XCD,
+  // work-groups, one per CU (two with the dual map), take work items from 8 queues, one per XCD,
   // whose counters (kQueueStride bytes apart, zeroed before the launch) are
   // at `queues`; null: one work-group per item, mapped by map_work.
   uint32_t* queues;

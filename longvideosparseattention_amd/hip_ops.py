@@ -47,17 +47,20 @@ def attn_block_q(head_dim: int = 128, dtype: Optional[torch.dtype] = None, frame
                  key_rows: int = 0, n_k: int = 0, k_tok0: int = 0) -> int:
     """Query rows per attention tile, i.e. which kernel a plan is built for.
 
-    384 for head size 64 in 16-bit when query frames span at least 383 rows
-    and key frames at least 64 (``frame_rows``, ``key_rows``), and the short
-    last block of a key source of ``n_k`` rows from token ``k_tok0`` lies in
-    one frame: the 12-wave single-stream kernel, three waves per SIMD.  256
-    for head sizes 64, 96 and 128 otherwise: the 8-wave kernels (bf16 /
-    fp16).  128 for 192 and 256: the single-stream kernel's wide map (4
-    waves, one per SIMD, when query frames span at least 127 rows and key
-    frames at least 64) or else the 4-wave kernel, and for fp32 inputs at
-    every head size (the fp32 kernel).  ``LVSA_ATTN_BLOCK_Q`` (128, 256 or
-    384) overrides the choice for 64 and 128 in 16-bit (384: head size 64
-    only); 96 runs on the 8-wave kernel only."""
+    256 for head sizes 64, 96 and 128 in 16-bit: the single-stream kernels
+    (head size 64: the dual map, 4 waves of 64 rows, two work-groups per CU)
+    when query frames span at least 255 rows and key frames at least 64, the
+    8-wave ping-pong kernel otherwise.  128 for 192 and 256: the
+    single-stream kernel's wide map (4 waves, one per SIMD, when query frames
+    span at least 127 rows and key frames at least 64) or else the 4-wave
+    kernel, and for fp32 inputs at every head size (the fp32 kernel).
+
+    ``LVSA_ATTN_BLOCK_Q`` (128, 256 or 384) overrides the choice for 64 and
+    128 in 16-bit, for comparisons.  384 selects the 12-wave single-stream
+    kernel (head size 64, three waves of 32 rows per SIMD) where the geometry
+    allows it: query frames of at least 383 rows (``frame_rows``), key frames
+    of at least 64 (``key_rows``), and a key source of ``n_k`` rows from token
+    ``k_tok0`` whose short last block lies in one frame; 256 otherwise."""
     kd = kernel_head_dim(head_dim)
     if dtype == torch.float32:
         return 128
@@ -66,11 +69,12 @@ def attn_block_q(head_dim: int = 128, dtype: Optional[torch.dtype] = None, frame
     if kd == 96:
         return 256
     env = os.environ.get("LVSA_ATTN_BLOCK_Q")
+    if env == "384":
+        ok = (kd == 64 and frame_rows >= 383 and key_rows >= capi.ATTN_BLOCK_K and
+              not stream_tail_crosses_frame(1, n_k, k_tok0, key_rows))
+        return 384 if ok else 256
     if env:
         return int(env)
-    if (kd == 64 and frame_rows >= 383 and key_rows >= capi.ATTN_BLOCK_K and
-            not stream_tail_crosses_frame(1, n_k, k_tok0, key_rows)):
-        return 384
     return 256
 
 

@@ -451,6 +451,8 @@ class Wave:
             m = self.sval64(a[3])
             bits = np.array([(m >> i) & 1 for i in range(64)], dtype=bool)
             self.vdst(a[0], np.where(bits, self.vsrc_u(a[2]), self.vsrc_u(a[1])))
+        elif op == 'v_add_u32':
+            self.vdst(a[0], (self.vsrc_u(a[1]).astype(np.int64) + self.vsrc_u(a[2])) & M32)
         elif op == 'v_sub_u32':
             self.vdst(a[0], (self.vsrc_u(a[1]).astype(np.int64) - self.vsrc_u(a[2])) & M32)
         elif op == 'v_mad_u32_u24':
@@ -473,7 +475,8 @@ class Wave:
 class Sim:
     def __init__(self, dt='bf16', **opts):
         # the product's loop for the head size, with any options of the test on top
-        lines = G.Gen(dt, **{**G.PRODUCT[opts.get("D", 128)], **opts}).build()
+        D, nw = opts.get("D", 128), opts.get("nw", 8)
+        lines = G.Gen(dt, **{**G.PRODUCT[D], **G.PRODUCT_MAP.get((D, nw), {}), **opts}).build()
         self.nw = opts.get("nw", 8)
         self.prog, self.labels = parse_program(lines)
         self.mem = Mem()

@@ -178,8 +178,8 @@ CP_SHARDS = [
     (6, 260, 1, 3, 1, 2, 128, 5, 0),
     (6, 260, 1, 3, 1, 2, 64, 5, 0),
     (6, 260, 1, 3, 1, 2, 192, 5, 0),
-    # P >= 383 (384-row tiles for head size 64) with a crossing last block:
-    # keys [384, 440), boundary at 385
+    # P >= 383 (where head size 64 may run 384-row tiles) with a crossing
+    # last block: keys [384, 440), boundary at 385
     (8, 385, 1, 3, 2, 2, 64, 7, 0),
 ]
 
@@ -748,7 +748,7 @@ def test_work_queues_match_static_grid(cfg, gpu):
 
 
 TALL = [
-    # T, P, W, kfi, off, H, Hkv, D, n_txt, dtype, B  (head size 64, frames >= 383 rows: 384-row tiles)
+    # T, P, W, kfi, off, H, Hkv, D, n_txt, dtype, B  (head size 64, frames >= 383 rows: 384-row tiles possible)
     (13, 1350, 1, 4, 0, 6, 6, 64, 226, torch.bfloat16, 1),     # CogVideoX frame and text sizes
     (9, 383, 2, 4, 1, 4, 2, 64, 37, torch.bfloat16, 2),        # smallest frame for 384 rows, GQA, batch 2
     (21, 700, 1, 3, 2, 3, 3, 64, 0, torch.float16, 1),         # fp16, video only, frames straddling tiles
@@ -757,12 +757,17 @@ TALL = [
 
 
 @pytest.mark.parametrize("cfg", TALL, ids=[str(c[:9]) for c in TALL])
-def test_twelve_wave_tiles_match_eight_wave_tiles(cfg, gpu):
-    """Head size 64 with frames of >= 383 rows runs 384-row tiles on the
-    12-wave kernel (three waves per SIMD).  Per query row it walks the same
-    key blocks in the same order as the 256-row plan (blocks masked out for a
-    row add exact zeros), so O and LSE equal the 8-wave kernel's bit for bit;
-    spot frames and text rows are also checked against the fp32 oracle."""
+def test_head64_maps_agree(cfg, gpu, monkeypatch):
+    """Head size 64 has three single-stream maps for frames of >= 383 rows:
+    the dual map (the default: 256-row tiles, 4 waves of 64 rows, two
+    work-groups per CU), 8 waves of 32 rows on the same plan
+    (LVSA_D64_WAVES=8) and 12 waves on 384-row tiles.  Per query row the
+    8- and 12-wave kernels walk the same key blocks in the same order
+    (blocks masked out for a row add exact zeros), so their O and LSE agree
+    bit for bit.  The dual map computes each 32-row half as the 8-wave kernel
+    does, except that a half also takes the exact-max path when the other
+    half of its wave needs it (a rescale, rounding only).  Spot frames and
+    text rows are checked against the fp32 oracle."""
     T, P, W, kfi, off, H, Hkv, D, n_txt, dt, B = cfg
     N = T * P
     m = _meta(T, P, W, 1, kfi, off)
@@ -770,25 +775,34 @@ def test_twelve_wave_tiles_match_eight_wave_tiles(cfg, gpu):
                                  (B, n_txt, Hkv, D), (B, n_txt, Hkv, D)], seed=17, dtype=dt)
     g = [x.to(gpu) for x in (q, k, v, qt, kt, vt)]
     plan = m.full_plan(gpu, N, N, n_txt, n_txt, D, dt)
-    assert plan.block_q == 384
+    assert plan.block_q == 256
     st = m.device_state(gpu)
-    plan256 = hip_ops.plan_build(st.mask.rel_full, n_q=N, n_k=N, n_x=n_txt, n_tq=n_txt, R=P, Cf=P,
-                                 max_row_frames=max(1, m.max_row_frames), block_q=256)
+    plan384 = hip_ops.plan_build(st.mask.rel_full, n_q=N, n_k=N, n_x=n_txt, n_tq=n_txt, R=P, Cf=P,
+                                 max_row_frames=max(1, m.max_row_frames), block_q=384)
     kw = dict(kx=g[4], vx=g[5], qt=g[3]) if n_txt else {}
-    o12, ot12, l12, lt12 = hip_ops.attn_fwd(g[0], g[1], g[2], plan, return_lse=True, **kw)
-    o8, ot8, l8, lt8 = hip_ops.attn_fwd(g[0], g[1], g[2], plan256, return_lse=True, **kw)
+    od, otd, ld, ltd = hip_ops.attn_fwd(g[0], g[1], g[2], plan, return_lse=True, **kw)
+    o12, ot12, l12, lt12 = hip_ops.attn_fwd(g[0], g[1], g[2], plan384, return_lse=True, **kw)
+    monkeypatch.setenv("LVSA_D64_WAVES", "8")
+    o8, ot8, l8, lt8 = hip_ops.attn_fwd(g[0], g[1], g[2], plan, return_lse=True, **kw)
+    monkeypatch.delenv("LVSA_D64_WAVES")
     assert torch.equal(o12, o8) and torch.equal(l12, l8), "video rows differ between 384- and 256-row tiles"
     if n_txt:
         assert torch.equal(ot12, ot8) and torch.equal(lt12, lt8), "text rows differ"
+    # dual map against 8 waves: rounding of an extra rescale at most
+    assert (od.float() - o8.float()).abs().max().item() <= 2e-3 and (ld - l8).abs().max().item() <= 1e-4
+    if n_txt:
+        assert (otd.float() - ot8.float()).abs().max().item() <= 2e-3 and (ltd - lt8).abs().max().item() <= 1e-4
     rows = [set(r) for r in om.build_frame_mask(T, P, W, 1, kfi, offset=off).rows]
     for b in range(B):
         ro, _ = oa.per_frame_sdpa(g[0][b:b + 1].float(), g[1][b:b + 1].float(), g[2][b:b + 1].float(), rows, P,
                                   k_extra=g[4][b:b + 1].float() if n_txt else None,
                                   v_extra=g[5][b:b + 1].float() if n_txt else None, frames=[0, 1, T // 2, T - 1])
+        _close(od[b:b + 1], ro, f"dual map, batch {b}")
         _close(o12[b:b + 1], ro, f"384-row tiles, batch {b}")
     if n_txt:
         rto, _ = oa.text_row_attention(g[3][:1].float(), g[1][:1].float(), g[2][:1].float(), g[4][:1].float(),
                                        g[5][:1].float())
+        _close(otd[:1], rto, "dual map, text rows")
         _close(ot12[:1], rto, "384-row tiles, text rows")
 
 

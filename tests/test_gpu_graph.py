@@ -51,9 +51,9 @@ def _assert_same(a, b, what):
 
 
 # 128-token frames run the ping-pong / 4-wave kernels; 400-token frames the
-# single-stream kernels (D = 128 and 96 on 256-row tiles, D = 64 on 384-row
-# tiles with 12 waves), whose work-queue counters are zeroed by a kernel in
-# the captured graph.
+# single-stream kernels (D = 128 and 96 on 256-row tiles with 8 waves, D = 64
+# on 256-row tiles with the dual map's 4 waves of 64 rows), whose work-queue
+# counters are zeroed by a kernel in the captured graph.
 @pytest.mark.parametrize("D,offset,P", [(128, 0, 128), (128, 3, 128), (64, 1, 128), (96, 2, 128), (192, 3, 128),
                                         (256, 0, 128), (128, 1, 400), (96, 3, 400), (64, 2, 400)])
 def test_step_graph_replays_match_eager(D, offset, P):

@@ -28,7 +28,7 @@ def _draw(shapes, seed):
 
 
 # 128-token frames: the ping-pong kernel; 400-token frames: the single-stream
-# kernels (D = 128 on 256-row tiles, D = 64 on 384-row tiles)
+# kernels (256-row tiles: D = 128 with 8 waves, D = 64 with the dual map)
 @pytest.mark.parametrize("P", [128, 400])
 @pytest.mark.parametrize("D", [128, 64])
 @pytest.mark.parametrize("n_txt", [48, 0])

@@ -150,18 +150,34 @@ def test_head_sizes_of_the_plugin():
     assert [hip_ops.kernel_head_dim(d) for d in (64, 96, 128, 192, 256)] == [64, 96, 128, 192, 256]
     assert hip_ops.attn_block_q(256) == 128 and hip_ops.attn_block_q(192) == 128
     assert hip_ops.attn_block_q(96) == 256
-    # head size 64: 384-row tiles (12 waves) when frames span >= 383 query and >= 64 key rows
+    # head size 64: 256-row tiles (the dual map); fp32: 128
+    assert hip_ops.attn_block_q(64, torch.bfloat16, 1350, 1350) == 256
+    assert hip_ops.attn_block_q(64, torch.float16, 383, 64) == 256
+    assert hip_ops.attn_block_q(64, torch.float32, 1350, 1350) == 128
+    assert hip_ops.attn_block_q(128, torch.bfloat16, 1560, 1560) == 256
+    with pytest.raises(ValueError, match="head_dim 80"):
+        hip_ops.kernel_head_dim(80)
+
+
+def test_block_q_override_384(monkeypatch):
+    """LVSA_ATTN_BLOCK_Q=384 selects the 12-wave kernel's 384-row tiles for
+    head size 64 where the geometry allows them (query frames >= 383 rows, key
+    frames >= 64, the key source's short last block inside one frame) and
+    256-row tiles elsewhere."""
+    from longvideosparseattention_amd import hip_ops
+
+    monkeypatch.setenv("LVSA_ATTN_BLOCK_Q", "384")
     assert hip_ops.attn_block_q(64, torch.bfloat16, 1350, 1350) == 384
     assert hip_ops.attn_block_q(64, torch.float16, 383, 64) == 384
     assert hip_ops.attn_block_q(64, torch.bfloat16, 382, 1350) == 256
     assert hip_ops.attn_block_q(64, torch.bfloat16, 1350, 63) == 256
-    assert hip_ops.attn_block_q(64, torch.float32, 1350, 1350) == 128
     assert hip_ops.attn_block_q(128, torch.bfloat16, 1560, 1560) == 256
+    assert hip_ops.attn_block_q(64, torch.float32, 1350, 1350) == 128
     # a shard whose short last key block crosses a frame boundary: 256-row tiles
     assert hip_ops.attn_block_q(64, torch.bfloat16, 385, 385, n_k=440, k_tok0=0) == 256
     assert hip_ops.attn_block_q(64, torch.bfloat16, 385, 385, n_k=440, k_tok0=440) == 384
-    with pytest.raises(ValueError, match="head_dim 80"):
-        hip_ops.kernel_head_dim(80)
+    monkeypatch.setenv("LVSA_ATTN_BLOCK_Q", "128")
+    assert hip_ops.attn_block_q(64, torch.bfloat16, 1350, 1350) == 128
 
 
 def _frame_parts_of_last_block(n_k, k_tok0, C, block=64):

@@ -51,10 +51,12 @@ def _allowed(y, row, key_in_block):
 def run_loop(entries, nk, n_x, seed=0, dt="bf16", D=128, nw=8, **opts):
     """Run the generated loop for the `nw` waves of one work-group with the
     registers the C++ prologue of attn_fwd_stream_kernel sets up (the 12-wave
-    kernel: 384 query rows, waves 8-11 repeat the copies of waves 0-3)."""
+    kernel: 384 query rows, waves 8-11 repeat the copies of waves 0-3; the
+    dual map, D = 64 with 4 waves: 64 rows per wave as two 32-row halves)."""
     rng = np.random.default_rng(seed)
-    R = 32 * nw
     L = A.G.Layout(D, nw, rs=opts.get("rs_mfma", A.G.PRODUCT[D].get("rs_mfma", False)))
+    NR = L.NR
+    R = 32 * NR * nw
     RB, NCH = L.RB, L.RB // 16            # LDS row pitch (D = 96: the D = 128 pitch), chunks per row
     GRB = 2 * D                           # global row stride of K and V
     rnd = (lambda x: A.bf16_to_f32(A.bf16_round(x))) if dt == "bf16" else (lambda x: x.astype(np.float16).astype(np.float32))
@@ -73,11 +75,12 @@ def run_loop(entries, nk, n_x, seed=0, dt="bf16", D=128, nw=8, **opts):
     for w in range(nw):
         W = A.Wave(w, sim)
         V = W.v
-        rows = 32 * w + i32
-        for c in range(L.NQK):
-            for j in range(4):
-                d0 = 16 * c + 8 * h + 2 * j
-                V[L.Q + 4 * c + j] = qbits[rows, d0] | (qbits[rows, d0 + 1] << 16)
+        for r in range(NR):
+            rows = 32 * NR * w + 32 * r + i32
+            for c in range(L.NQK):
+                for j in range(4):
+                    d0 = 16 * c + 8 * h + 2 * j
+                    V[L.Q + 4 * L.NQK * r + 4 * c + j] = qbits[rows, d0] | (qbits[rows, d0 + 1] << 16)
         sw = np.array([_swz(x & 15, D) for x in i32])
         for c in range(L.NQK):
             V[L.KOFF + c] = i32 * RB + (((2 * c + h) ^ sw) << 4)
@@ -104,8 +107,9 @@ def run_loop(entries, nk, n_x, seed=0, dt="bf16", D=128, nw=8, **opts):
             V[L.C16] = ((lane % NCH) ^ np.array([_swz(x & 15, D) for x in crow])) * 16
             if ndata < NCH:   # chunks past the row's data: an offset beyond every source (zeros, no access)
                 V[L.C16] = np.where(V[L.C16] >= 16 * ndata, 0x7FFF0000, V[L.C16])
-        V[L.ROW], V[L.H4], V[L.NEGINF], V[L.VT] = 32 * w + i32, 4 * h, 0xFF800000, 0
-        V[L.VM] = A.f2u(np.full(64, -1e30, np.float32))
+        V[L.ROW], V[L.H4], V[L.NEGINF], V[L.VT] = 32 * NR * w + i32, 4 * h, 0xFF800000, 0
+        for r in range(NR):
+            V[L.VM + r] = A.f2u(np.full(64, -1e30, np.float32))
         if L.rs:
             one = 0x3F803F80 if dt == "bf16" else 0x3C003C00
             for j in range(4):
@@ -124,12 +128,14 @@ def run_loop(entries, nk, n_x, seed=0, dt="bf16", D=128, nw=8, **opts):
     obase = 256 if L.wide else 0          # the wide map keeps O in AGPRs
     for w, W in enumerate(waves):
         for ln in range(64):
-            r, hh = 32 * w + (ln & 31), ln >> 5
-            for dt_ in range(L.NDT):
-                for rr in range(16):
-                    O[r, 32 * dt_ + 8 * (rr // 4) + 4 * hh + rr % 4] = A.u2f(W.v[obase + L.O + 16 * dt_ + rr, ln])
-            lsum[r] += A.u2f(W.v[L.VL, ln])
-            mrun[r] = A.u2f(W.v[L.VM, ln])
+            for hr in range(NR):
+                r, hh = 32 * NR * w + 32 * hr + (ln & 31), ln >> 5
+                for dt_ in range(L.NDT):
+                    for rr in range(16):
+                        O[r, 32 * dt_ + 8 * (rr // 4) + 4 * hh + rr % 4] = \
+                            A.u2f(W.v[obase + L.O + 16 * L.NDT * hr + 16 * dt_ + rr, ln])
+                lsum[r] += A.u2f(W.v[L.VL + hr, ln])
+                mrun[r] = A.u2f(W.v[L.VM + hr, ln])
     # reference: float64 softmax attention over the allowed keys
     ref = np.zeros((R, D))
     lse_ref = np.zeros(R)
@@ -185,6 +191,26 @@ def test_loop_12_waves(case):
     err, lse_err, copies = run_loop(make(), nk, n_x, D=64, nw=12)
     assert err <= 4e-3 and lse_err <= 2e-3, (case, err, lse_err)
     assert copies == 12 * 2 * (len(make()) + 2)
+
+
+@pytest.mark.parametrize("case", sorted(CASES))
+def test_loop_dual(case):
+    """The dual map: D = 64, 4 waves of 64 rows (two 32-row halves sharing
+    each LDS operand), 256-row tiles."""
+    make, nk, n_x = CASES[case]
+    err, lse_err, copies = run_loop(make(), nk, n_x, D=64, nw=4)
+    assert err <= 4e-3 and lse_err <= 2e-3, (case, err, lse_err)
+    # two copies of K and two of V per wave and block, blocks 0..n+1
+    assert copies == 4 * 4 * (len(make()) + 2)
+
+
+def test_loop_dual_rare_path_and_fp16():
+    """The dual map with the exact-max path on every sub-block (both halves),
+    and with fp16 inputs."""
+    err, lse_err, _ = run_loop([(j, 0) for j in range(3)], 192, 0, seed=6, D=64, nw=4, always_rare=True)
+    assert err <= 4e-3 and lse_err <= 2e-3, (err, lse_err)
+    err, lse_err, _ = run_loop([(j, _tail(150, j)) for j in range(3)], 150, 0, seed=7, dt="f16", D=64, nw=4)
+    assert err <= 2e-3 and lse_err <= 2e-3, (err, lse_err)
 
 
 def test_loop_12_waves_row_split_past_255_and_rare_path():
