@@ -15,7 +15,8 @@ namespace {
 
 // Key blocks (of 64 keys) per text chunk when a text tile is split: about a
 // third of a Wan / HunyuanVideo video tile and below a CogVideoX one, so the
-// chunks fill the launch's last round at a granularity finer than a tile.
+// chunks fill the launch's last round at a granularity finer than a tile
+// (64 measured the same at CogVideoX and 0.3% slower at HunyuanVideo).
 constexpr int kTextChunkBlocks = 128;
 constexpr int kMaxTextChunks = 64;
 
@@ -32,10 +33,24 @@ int64_t text_ws_bytes(const lvsa_attn_args* a, int chunks) {
   return 4 * (text_ws_o_elems(chunks, a->B, a->H, a->n_tq, a->D) + 2LL * chunks * a->B * a->H * a->n_tq);
 }
 
+// Partials of the video split with `vsplit` slots per queue (O, then the
+// (running max, row sum) pairs).
+int64_t video_ws_bytes(const lvsa_attn_args* a, int vsplit) {
+  if (vsplit <= 0) return 0;
+  return 4 * (video_ws_o_elems(vsplit, a->block_q, a->D) + 2LL * kXcds * vsplit * 2 * a->block_q);
+}
+
 // Workspace of a call: the text-split partials (text_ws_bytes) at offset 0,
-// then the work-queue counters (kQueueBytes) at a 256-byte boundary.
-int64_t queue_offset(int64_t text_bytes) { return (text_bytes + 255) & ~int64_t(255); }
-int64_t ws_bytes(const lvsa_attn_args* a) { return queue_offset(text_ws_bytes(a, text_chunks_of(a))) + kQueueBytes; }
+// the video-split partials (video_ws_bytes) after them at a 256-byte
+// boundary, then the work-queue counters (kQueueBytes) at the next one.
+int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
+int64_t video_offset(const lvsa_attn_args* a, int chunks) { return align256(text_ws_bytes(a, chunks)); }
+int64_t queue_offset(const lvsa_attn_args* a, int chunks, int vsplit) {
+  return align256(video_offset(a, chunks) + video_ws_bytes(a, vsplit));
+}
+int64_t ws_bytes(const lvsa_attn_args* a, int vsplit) {
+  return queue_offset(a, text_chunks_of(a), vsplit) + kQueueBytes;
+}
 
 // Zero the work-queue counters (a kernel, not a memset, so the call can be
 // captured in a HIP graph and replayed).
@@ -56,6 +71,33 @@ int cu_count() {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0) cached[dev] = n;
   }
   return cached[dev];
+}
+
+// Whether a 16-bit head size 64 plan of 256-row tiles runs the dual map
+// (LVSA_D64_WAVES=8 selects 8 waves of 32 rows instead, for comparisons).
+bool dual_map(const lvsa_attn_args* a) {
+  const char* w = getenv("LVSA_D64_WAVES");
+  return a->D == 64 && a->block_q == kPPBM && a->dtype != LVSA_FP32 && !(w && strcmp(w, "8") == 0);
+}
+
+// Video tiles split in key-range halves at the end of each work queue, with
+// the dual map: its two work-groups per CU take whole tiles at half the CU's
+// rate, so a last round of whole tiles leaves CUs idle for longer.  As many
+// per queue as the queue has work-groups on its XCD, halved (32), so that the
+// last round runs half tiles, and at most the queue's video tiles
+// (CogVideoX 0.9% faster; the 8-wave maps, one work-group per CU, gain
+// nothing from it: Wan 4x and HunyuanVideo within +-0.5%).  0 for other maps,
+// fp32, calls too small for the work queues, or with LVSA_VIDEO_SPLIT=0.
+int vsplit_pref(const lvsa_attn_args* a) {
+  const char* e = getenv("LVSA_VIDEO_SPLIT");
+  if ((e && strcmp(e, "0") == 0) || !dual_map(a) || a->n_q == 0) return 0;
+  const int per_cu = 2;
+  const int64_t cus = cu_count();
+  const int64_t vwork = ceil_div(a->n_q, a->block_q) * a->H * a->B;
+  const int64_t work = vwork + ceil_div(a->n_tq, a->block_q) * text_chunks_of(a) * a->H * a->B;
+  if (cus <= 0 || work <= per_cu * cus) return 0;
+  const int64_t s = per_cu * cus / (2 * kXcds), per_queue = ceil_div(vwork, kXcds);
+  return (int)(s < per_queue ? s : per_queue);
 }
 
 // Exact log-sum-exp merge of the text chunks (lvsa-vllm-omni/lvsa_vllm_omni/
@@ -99,6 +141,43 @@ __global__ __launch_bounds__(256) void attn_text_merge_kernel(const float* ws, i
   op[3] = (E)(acc.w * inv);
   if (lse_t && dq == 0)
     lse_t[bh * n_tq + row] = L > 0.f ? (M + __log2f(L)) * 0.69314718055994530942f : -INFINITY;
+}
+
+// Merge of the two halves of the split video tiles (vsplit slots per queue):
+// one thread per (slot, row, 4 columns), the exact log-sum-exp combination
+// of attn_text_merge_kernel, written where the unsplit tile writes O and LSE.
+template <typename E>
+__global__ __launch_bounds__(256) void attn_video_merge_kernel(AttnParams p, int block_q, int D) {
+  const int g4 = D / 4;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t per_slot = (int64_t)block_q * g4;
+  const int64_t slot = t / per_slot;   // x * vsplit + s
+  if (slot >= (int64_t)kXcds * p.vsplit) return;
+  const int x = (int)(slot / p.vsplit), sx = (int)(slot % p.vsplit);
+  const QueueShape q = queue_shape(p, x);
+  if (sx >= q.n_split) return;
+  const int w = q.v0 + q.n_video - q.n_split + sx;
+  const int tile = w % p.n_vt, rest = w / p.n_vt, head = rest % p.H, batch = rest / p.H;
+  const int r = (int)((t % per_slot) / g4), dq = (int)(t % g4);
+  const int64_t row = (int64_t)tile * block_q + r;
+  if (row >= p.n_q) return;
+  const float2* ml = reinterpret_cast<const float2*>(p.vws + video_ws_o_elems(p.vsplit, block_q, D));
+  const int64_t i0 = (2 * slot) * block_q + r, i1 = i0 + block_q;
+  const float2 a0 = ml[i0], a1 = ml[i1];
+  const float M = fmaxf(a0.x, a1.x);
+  const float w0 = __builtin_amdgcn_exp2f(a0.x - M), w1 = __builtin_amdgcn_exp2f(a1.x - M);
+  const float L = w0 * a0.y + w1 * a1.y;
+  const float4 o0 = *reinterpret_cast<const float4*>(p.vws + i0 * D + 4 * dq);
+  const float4 o1 = *reinterpret_cast<const float4*>(p.vws + i1 * D + 4 * dq);
+  const float inv = L > 0.f ? 1.0f / L : 0.f;
+  E* op = reinterpret_cast<E*>(p.o + 2 * (batch * p.o_str[0] + row * p.o_str[1] + head * p.o_str[2])) + 4 * dq;
+  op[0] = (E)((w0 * o0.x + w1 * o1.x) * inv);
+  op[1] = (E)((w0 * o0.y + w1 * o1.y) * inv);
+  op[2] = (E)((w0 * o0.z + w1 * o1.z) * inv);
+  op[3] = (E)((w0 * o0.w + w1 * o1.w) * inv);
+  if (p.lse && dq == 0)
+    p.lse[((int64_t)batch * p.H + head) * p.n_q + row] =
+        L > 0.f ? (M + __log2f(L)) * 0.69314718055994530942f : -INFINITY;
 }
 
 // Whether the short last key block of the frame-structured source crosses a
@@ -189,7 +268,7 @@ extern "C" int lvsa_attn_fwd(const lvsa_attn_args* a, hipStream_t stream) {
                  (long long)first, (long long)last, a->rel_rows);
   }
   const int chunks = a->workspace ? text_chunks_of(a) : 1;
-  const int64_t ws_need = a->workspace ? ws_bytes(a) : 0;
+  const int64_t ws_need = a->workspace ? ws_bytes(a, 0) : 0;   // without the video split
   LVSA_REQUIRE(a->workspace_bytes >= ws_need, LVSA_ERR_CAPACITY,
                "lvsa_attn_fwd: workspace of %lld bytes < %lld needed (lvsa_attn_workspace_query)",
                (long long)a->workspace_bytes, (long long)ws_need);
@@ -248,6 +327,8 @@ extern "C" int lvsa_attn_fwd(const lvsa_attn_args* a, hipStream_t stream) {
   p.text_chunks = chunks;
   p.text_first = chunks == 1 ? 1 : 0;
   p.ws = chunks > 1 ? (float*)a->workspace : nullptr;
+  p.vsplit = 0;
+  p.vws = nullptr;
   // The single-stream kernel (D = 64, 96 and 128 here; 192 and 256 below)
   // serves plans without generic descriptors:
   // 256-row tiles touch at most two query frames when frames have >= 255
@@ -295,8 +376,7 @@ extern "C" int lvsa_attn_fwd(const lvsa_attn_args* a, hipStream_t stream) {
   // D = 64 on 256-row tiles: the dual map (64 rows per wave, 4 waves, two
   // work-groups per CU); LVSA_D64_WAVES=8 selects 8 waves of 32 rows instead
   // (comparisons).
-  const char* wenv = getenv("LVSA_D64_WAVES");
-  p.dual = (p.use_stream && a->D == 64 && a->block_q == kPPBM && !(wenv && strcmp(wenv, "8") == 0)) ? 1 : 0;
+  p.dual = (p.use_stream && dual_map(a)) ? 1 : 0;
   // With a workspace, the single-stream kernel runs one persistent
   // work-group per CU (two with the dual map) over the work queues (counters
   // zeroed first).
@@ -305,7 +385,14 @@ extern "C" int lvsa_attn_fwd(const lvsa_attn_args* a, hipStream_t stream) {
   const int cus = cu_count();
   const int per_cu = p.dual ? 2 : 1;
   if (p.use_stream && a->workspace && cus > 0 && work > per_cu * cus) {
-    p.queues = (uint32_t*)((char*)a->workspace + queue_offset(text_ws_bytes(a, chunks)));
+    // the video split when the workspace holds its partials (the size
+    // lvsa_attn_workspace_query returns), none otherwise
+    const int vs = vsplit_pref(a);
+    if (vs > 0 && a->workspace_bytes >= ws_bytes(a, vs)) {
+      p.vsplit = vs;
+      p.vws = (float*)((char*)a->workspace + video_offset(a, chunks));
+    }
+    p.queues = (uint32_t*)((char*)a->workspace + queue_offset(a, chunks, p.vsplit));
     p.grid = per_cu * cus;
     hipLaunchKernelGGL(queue_reset_kernel, dim3(1), dim3(64), 0, stream, p.queues);
     const int qrc = launch_status("lvsa_attn_fwd (queue reset)");
@@ -320,7 +407,16 @@ extern "C" int lvsa_attn_fwd(const lvsa_attn_args* a, hipStream_t stream) {
   else if (a->D == 96) rc = launch_d96(p, bq, bf16, stream);
   else if (a->D == 192) rc = launch_d192(p, bq, bf16, stream);
   else rc = launch_d64(p, bq, bf16, stream);
-  if (rc != LVSA_OK || chunks == 1) return rc;
+  if (rc != LVSA_OK) return rc;
+  if (p.vsplit > 0) {
+    const int64_t threads = (int64_t)kXcds * p.vsplit * bq * (a->D / 4);
+    const dim3 grid((unsigned)ceil_div(threads, 256));
+    if (bf16) hipLaunchKernelGGL(attn_video_merge_kernel<__bf16>, grid, dim3(256), 0, stream, p, bq, a->D);
+    else hipLaunchKernelGGL(attn_video_merge_kernel<_Float16>, grid, dim3(256), 0, stream, p, bq, a->D);
+    rc = launch_status("lvsa_attn_fwd (video merge)");
+    if (rc != LVSA_OK) return rc;
+  }
+  if (chunks == 1) return rc;
   const int64_t threads = (int64_t)a->B * a->H * a->n_tq * (a->D / 4);
   const dim3 grid((unsigned)ceil_div(threads, 256));
   if (bf16) {
@@ -335,6 +431,10 @@ extern "C" int lvsa_attn_fwd(const lvsa_attn_args* a, hipStream_t stream) {
   return launch_status("lvsa_attn_fwd (text merge)");
 }
 
+namespace lvsa {
+int64_t attn_workspace_min_bytes(const lvsa_attn_args* a) { return ws_bytes(a, 0); }
+}  // namespace lvsa
+
 extern "C" int lvsa_attn_workspace_query(const lvsa_attn_args* a, int64_t* bytes) {
   clear_error();
   LVSA_REQUIRE(a != nullptr && bytes != nullptr, LVSA_ERR_INVALID_ARG, "lvsa_attn_workspace_query: null pointer");
@@ -342,6 +442,6 @@ extern "C" int lvsa_attn_workspace_query(const lvsa_attn_args* a, int64_t* bytes
                "lvsa_attn_workspace_query: bad sizes");
   LVSA_REQUIRE(a->D == 64 || a->D == 96 || a->D == 128 || a->D == 192 || a->D == 256, LVSA_ERR_UNSUPPORTED,
                "lvsa_attn_workspace_query: head_dim %d not supported", a->D);
-  *bytes = ws_bytes(a);
+  *bytes = ws_bytes(a, vsplit_pref(a));
   return LVSA_OK;
 }

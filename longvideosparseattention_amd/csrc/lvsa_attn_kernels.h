@@ -78,6 +78,14 @@ struct AttnParams {
   // D = 64, 256-row tiles on the single-stream kernel: the dual map (4 waves
   // of 64 rows, two work-groups per CU) rather than 8 waves of 32 rows
   int dual;
+  // Key-range split of each queue's last video tiles (with the work queues):
+  // the last min(vsplit, videos of the queue) video items of queue x run as
+  // two halves of their entry lists, after the queue's whole tiles, and write
+  // unnormalised partials to slots x * vsplit + s of vws (fp32 O [slot][half]
+  // [block_q][D], then (running max, row sum) [slot][half][block_q]) for
+  // attn_video_merge_kernel.  0: no split.
+  int vsplit;
+  float* vws;
   // Work queues (single-stream kernel with a workspace): `grid` persistent
   // work-groups, one per CU (two with the dual map), take work items from 8 queues, one per XCD,
   // whose counters (kQueueStride bytes apart, zeroed before the launch) are
@@ -238,6 +246,7 @@ __device__ __forceinline__ void wait_vm0() {
 struct WorkItem {
   int tile, head, batch, chunk;
   bool text;
+  int vhalf, vslot;   // a split video tile: half 0 or 1 and its partial slot; vhalf -1: whole
 };
 __device__ __forceinline__ WorkItem map_work(const AttnParams& p) {
   WorkItem it;
@@ -253,6 +262,8 @@ __device__ __forceinline__ WorkItem map_work(const AttnParams& p) {
     it.head = t % p.H;
     it.batch = t / p.H;
     it.text = true;
+    it.vhalf = -1;
+    it.vslot = 0;
     return it;
   }
   const int x = b % kXcds;
@@ -269,19 +280,23 @@ __device__ __forceinline__ WorkItem map_work(const AttnParams& p) {
   it.batch = rest / p.H;
   it.chunk = 0;
   it.text = false;
+  it.vhalf = -1;
+  it.vslot = 0;
   return it;
 }
 
 // Work queues.  Queue x (one per XCD) holds, in this order: the unsplit text
 // items t = x, x + 8, ... (the longest, first), the video items of the same
 // XCD-contiguous range map_work gives XCD x (consecutive tiles of a head, so
-// the K/V blocks they share stay in that XCD's L2), and the split text chunks
-// t = x, x + 8, ... (the shortest, last).  A work-group takes items from the
+// the K/V blocks they share stay in that XCD's L2), the last n_split of them
+// as two halves each (key-range halves of their entry lists), and the split
+// text chunks t = x, x + 8, ... (the shortest, last).  The halves and the
+// chunks make the launch's last round finer than whole tiles.  A work-group takes items from the
 // queue of its own XCD and, once that is empty, from the next ones in turn:
 // XCDs that run faster take over the items of the slower ones at the end, so
 // the launch does not wait for the slowest XCD's fixed share.
 struct QueueShape {
-  int n_first, v0, n_video, n_last;
+  int n_first, v0, n_video, n_split, n_last;   // n_split of the n_video video items run as two halves
 };
 __host__ __device__ inline QueueShape queue_shape(const AttnParams& p, int x) {
   QueueShape q;
@@ -291,8 +306,12 @@ __host__ __device__ inline QueueShape queue_shape(const AttnParams& p, int x) {
   const int per = p.n_vwork / kXcds, rem = p.n_vwork % kXcds;
   q.v0 = x * per + (x < rem ? x : rem);
   q.n_video = per + (x < rem ? 1 : 0);
+  q.n_split = p.vsplit < q.n_video ? p.vsplit : q.n_video;
   return q;
 }
+
+// Items in queue x.
+__host__ __device__ inline int queue_items(const QueueShape& q) { return q.n_first + q.n_video + q.n_split + q.n_last; }
 
 __host__ __device__ inline WorkItem text_item(const AttnParams& p, int t) {
   WorkItem it;
@@ -303,6 +322,8 @@ __host__ __device__ inline WorkItem text_item(const AttnParams& p, int t) {
   it.head = t % p.H;
   it.batch = t / p.H;
   it.text = true;
+  it.vhalf = -1;
+  it.vslot = 0;
   return it;
 }
 
@@ -311,9 +332,18 @@ __host__ __device__ inline WorkItem queue_item(const AttnParams& p, int x, int j
   const QueueShape q = queue_shape(p, x);
   if (j < q.n_first) return text_item(p, x + kXcds * j);
   j -= q.n_first;
-  if (j >= q.n_video) return text_item(p, x + kXcds * (j - q.n_video));
+  const int n_whole = q.n_video - q.n_split;
+  if (j >= n_whole + 2 * q.n_split) return text_item(p, x + kXcds * (j - n_whole - 2 * q.n_split));
   WorkItem it;
-  const int w = q.v0 + j;
+  it.vhalf = -1;
+  it.vslot = 0;
+  int w = q.v0 + j;
+  if (j >= n_whole) {                 // half j & 1 of split tile s of the queue
+    const int s = (j - n_whole) >> 1;
+    w = q.v0 + n_whole + s;
+    it.vhalf = (j - n_whole) & 1;
+    it.vslot = x * p.vsplit + s;
+  }
   it.tile = w % p.n_vt;
   const int rest = w / p.n_vt;
   it.head = rest % p.H;
@@ -332,7 +362,7 @@ __device__ __forceinline__ int queue_next(const AttnParams& p, int& x, int& dry)
   while (dry < kXcds) {
     const QueueShape q = queue_shape(p, x);
     const uint32_t j = atomicAdd(p.queues + x * (kQueueStride / 4), 1u);
-    if (j < (uint32_t)(q.n_first + q.n_video + q.n_last)) return (int)(j << 3) | x;
+    if (j < (uint32_t)queue_items(q)) return (int)(j << 3) | x;
     x = (x + 1) & (kXcds - 1);
     ++dry;
   }
@@ -360,6 +390,25 @@ __device__ __forceinline__ void store_text_partial(char* wo, float* ml, int h, c
   if (h == 0) *reinterpret_cast<float2*>(ml) = float2{m_run, l_tot};
 }
 
+// Elements of the O partials of the video split: vsplit slots per queue, two
+// halves per slot, block_q rows of D.
+__host__ __device__ inline int64_t video_ws_o_elems(int vsplit, int block_q, int D) {
+  return (int64_t)kXcds * vsplit * 2 * block_q * D;
+}
+
+// A half of a split video tile writes its partials where a tile writes its
+// output: row base, row stride and LSE pointer redirected to its slot, offset
+// so that the tile's first row r0 lands on the slot's row 0.
+template <int D>
+__device__ __forceinline__ void video_partial_dst(const AttnParams& p, const WorkItem& it, int block_q, int64_t r0,
+                                                  char*& obase, int64_t& ors, float*& lse) {
+  const int64_t slot = 2 * (int64_t)it.vslot + it.vhalf;
+  const uintptr_t ws = reinterpret_cast<uintptr_t>(p.vws);
+  ors = 4 * D;
+  obase = reinterpret_cast<char*>(ws + 4 * (slot * block_q - r0) * D);
+  lse = reinterpret_cast<float*>(ws + 4 * (video_ws_o_elems(p.vsplit, block_q, D) + 2 * (slot * block_q - r0)));
+}
+
 // A split text item writes its partials where a tile writes its output: the
 // row base, row stride and LSE pointer of the text branch are redirected to
 // the scratch slots of (chunk, batch, head) (no extra state stays live
@@ -373,12 +422,17 @@ __device__ __forceinline__ void text_partial_dst(const AttnParams& p, const Work
   lse = p.ws + text_ws_o_elems(p.text_chunks, p.B, p.H, p.n_tq, D) + 2 * slot;
 }
 
-// Entry range [e0, e1) of the work item: the tile's plan entries, or chunk
-// `chunk` of text_chunks equal parts of them.
+// Entry range [e0, e1) of the work item: the tile's plan entries, chunk
+// `chunk` of text_chunks equal parts of them, or half `vhalf` of a split
+// video tile's (the first half takes the odd entry).
 __device__ __forceinline__ void item_entries(const AttnParams& p, const WorkItem& it, int& e0, int& e1) {
   e0 = p.tile_indptr[it.tile];
   e1 = p.tile_indptr[it.tile + 1];
-  if (it.text && p.text_chunks > 1) {
+  if (it.vhalf >= 0) {
+    const int mid = e0 + (e1 - e0 + 1) / 2;
+    if (it.vhalf == 0) e1 = mid;
+    else e0 = mid;
+  } else if (it.text && p.text_chunks > 1) {
     const int len = (e1 - e0 + p.text_chunks - 1) / p.text_chunks;
     const int a = e0 + it.chunk * len;
     e0 = a < e1 ? a : e1;

@@ -46,4 +46,9 @@ __host__ __device__ inline uint32_t make_desc(uint32_t kind, uint32_t bits, uint
   return kind | (bits << 2) | (ksplit << 8) | (qsplit << 16);
 }
 
+// Smallest workspace lvsa_attn_fwd runs a call with: the text-split partials
+// and the work-queue counters, without the video split's partials (which
+// lvsa_attn_workspace_query adds and lvsa_attn_fwd uses when they fit).
+int64_t attn_workspace_min_bytes(const lvsa_attn_args* a);
+
 }  // namespace lvsa

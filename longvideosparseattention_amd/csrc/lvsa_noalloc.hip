@@ -46,8 +46,11 @@ extern "C" int lvsa_attn_fwd_noalloc(const lvsa_attn_args* a, hipStream_t stream
   clear_error();
   LVSA_REQUIRE(a != nullptr, LVSA_ERR_INVALID_ARG, "lvsa_attn_fwd_noalloc: null args");
   int64_t need = 0;
-  int rc = lvsa_attn_workspace_query(a, &need);
+  int rc = lvsa_attn_workspace_query(a, &need);   // validates the arguments
   if (rc != LVSA_OK) return rc;
+  // the scratch must hold the text-tile split and the queue counters; the
+  // video split's partials are used when they fit as well
+  need = attn_workspace_min_bytes(a);
   LVSA_REQUIRE(need <= (int64_t)LVSA_NOALLOC_SCRATCH_BYTES, LVSA_ERR_CAPACITY,
                "lvsa_attn_fwd_noalloc: the text-tile split needs %lld bytes of scratch, more than the static "
                "%lld (LVSA_NOALLOC_SCRATCH_BYTES); call lvsa_attn_fwd with a workspace instead",

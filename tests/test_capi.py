@@ -172,11 +172,12 @@ def test_attn_workspace_query_and_capacity():
     assert chunks == 3
     text = 4 * chunks * 2 * 100 * (128 + 2)          # partial O and (max, sum) per chunk
     queues = 8 * 128                                  # one work-queue counter per 128-byte line
+    # 8 video tiles: too few for the work queues, so no video split either
     assert n.value == -(-text // 256) * 256 + queues
     a.workspace, a.workspace_bytes = 4096, n.value - 16
     assert lib.lvsa_attn_fwd(C.byref(a), None) == -3
     assert b"workspace" in lib.lvsa_last_error()
-    b = _attn_args(n_q=1000, rel_rows=10)     # no text queries: the queue counters only
+    b = _attn_args(n_q=0, rel_rows=10, n_tq=0)    # no queries: the queue counters only
     assert lib.lvsa_attn_workspace_query(C.byref(b), C.byref(n)) == 0 and n.value == queues
 
 
