@@ -222,10 +222,15 @@ typedef struct lvsa_attn_args {
    *   the long text tiles fill the launch's last round instead of
    *   lengthening it;
    * - the single-stream kernel (every 16-bit head size) runs one persistent
-   *   work-group per CU that takes work items from eight per-XCD queues
-   *   (counters in the last 1 KiB, zeroed by the call) and steals from the
-   *   other XCDs' queues once its own is empty, so XCDs that run faster take
-   *   over items of slower ones.
+   *   work-group per CU (two for head size 64) that takes work items from
+   *   eight per-XCD queues (counters in the last 1 KiB, zeroed by the call)
+   *   and steals from the other XCDs' queues once its own is empty, so XCDs
+   *   that run faster take over items of slower ones;
+   * - at head size 64 (two work-groups per CU) each queue's last video
+   *   tiles run as two key-range halves each, merged by a third launch as
+   *   the text chunks are, when the scratch holds their partials (the size
+   *   lvsa_attn_workspace_query returns; a smaller scratch of at least the
+   *   text split and the counters runs the tiles whole).
    * Null: one work-group per work item, text tiles whole and first.          */
   void* workspace;
   int64_t workspace_bytes;
@@ -238,8 +243,10 @@ typedef struct lvsa_attn_args {
 LVSA_API int lvsa_attn_fwd(const lvsa_attn_args* a, hipStream_t stream);
 
 /* Bytes of scratch lvsa_attn_fwd uses for `a`: the text-tile split
- * partials (none without text queries) and 1 KiB of work-queue counters;
- * host only, nothing is launched.
+ * partials (none without text queries), the video-tile split partials (head
+ * size 64, when the call has enough tiles for the work queues; their number
+ * follows the current device's compute units) and 1 KiB of work-queue
+ * counters; host only, nothing is launched.
  * Replaces the float workspace the FlashInfer wrapper is planned with
  * (flashinfer_runner.py:75-79, lvsa/lvsa_processor.py:798-804: 128 MB).      */
 LVSA_API int lvsa_attn_workspace_query(const lvsa_attn_args* a, int64_t* bytes);
@@ -250,8 +257,8 @@ LVSA_API int lvsa_attn_workspace_query(const lvsa_attn_args* a, int64_t* bytes);
  * scratch (work-queue counters and the text-tile split) comes from a static
  * device array of LVSA_NOALLOC_SCRATCH_BYTES per GPU (a->workspace is
  * ignored), which each GPU the library runs on holds until the process
- * ends; a call that needs more
- * returns LVSA_ERR_CAPACITY.  All calls on one GPU share that array: calls
+ * ends; a call whose text split and counters need more returns
+ * LVSA_ERR_CAPACITY (the video split runs only when it fits as well).  All calls on one GPU share that array: calls
  * that overlap on one GPU (other streams, other threads) race, so serialise
  * them.  The caller still passes inputs and outputs; nothing else differs
  * from lvsa_attn_fwd.                                                         */
