@@ -713,6 +713,7 @@ QUEUED = [
     # T, P, H, Hkv, D, n_txt, B   (well over 256 work items: the persistent work-queue launch)
     (24, 1100, 8, 2, 128, 300, 2),   # 1664 video tiles + split text chunks, GQA, batch 2
     (13, 1350, 24, 24, 64, 226, 1),  # CogVideoX frame size and text length, half the heads
+    (13, 1350, 16, 4, 64, 226, 2),   # the same, GQA (16 query heads over 4) and batch 2: split tiles of both
     (40, 1560, 12, 12, 128, 0, 1),   # Wan frame size, video only
 ]
 
