@@ -57,6 +57,14 @@ Register map (VGPRs; the kernel's operands pin them), D = 128 (D = 64):
   rs_mfma the two partial row sums give way to a ones pattern and a row-sum
   tile (4 each).  The 12-wave D = 64 map (Layout nw = 12) has four operand
   slots, eight softmax temps and the RARE temps inside them: 148 VGPRs.
+  The dual map (D = 64, Layout nw = 4) gives each wave 64 query rows as two
+  32-row halves: every operand item (an LDS read) feeds two MFMAs, one per
+  half (S + 16 r with Q + 16 r; O + 32 r with P + 8 r), and the softmax, the
+  rare path (either half's row sum over 2^8 takes both) and the mask run per
+  half (m and l of half r in VM + r and VL + r, its row sum in RS + 4 r, its
+  tile row in ROW + 32 r = ROW1); four operand slots, eight softmax temps:
+  249 VGPRs, two waves per SIMD (4 waves per work-group, two work-groups per
+  CU, 2 copies of K and 2 of V per wave and block).
   D = 96 (6 k-steps, 3 d-tiles) follows the D = 128 map with fewer O, Q and
   offset registers (202 VGPRs) and uses the D = 128 LDS layout: 256-byte rows
   whose chunks 12-15 the copies fill with zeros and no read touches.
@@ -97,7 +105,9 @@ class Layout:
     four operand slots read two MFMAs ahead, eight softmax temporaries, and the
     rare path's temporaries shared with them.  `nw` = 4 is the wide map of
     D = 192 and 256: one wave per SIMD, O in AGPRs, K and V in two-stage LDS
-    rings of their own (rows on the 512-byte pitch)."""
+    rings of their own (rows on the 512-byte pitch); at D = 64 it is the dual
+    map: 64 rows per wave in two 32-row halves (NR = 2), the compact map's
+    slots and temporaries, at most 256 VGPRs (two waves per SIMD)."""
 
     def __init__(self, D: int, nw: int = 8, rs: bool = False):
         assert (D, nw) in ((64, 8), (96, 8), (128, 8), (64, 12), (192, 4), (256, 4), (64, 4))
@@ -952,6 +962,11 @@ PRODUCT = {128: dict(lead=2, early_load=True, dot_init=True, and_scc=True, copy_
                      mask_fast=True, la=4, sm_start=4, copy_every=3, wait_pair=True),
            192: dict(early_load=True, dot_init=True, and_scc=True, copy_split=True, rs_mfma=True, tail_split=True,
                      mask_fast=True, la=4, sm_start=5, wait_pair=True, tail_nop=8)}
+# Measured and not used (paired runs on one box): s_setprio 1 or 3 around each
+# MFMA (`prio`; 12-wave CogVideoX 0.5-0.9% slower, Wan 4x 0.4%); lead PV
+# MFMAs and mid-block entry loads in the 12-wave loop (neutral); for the dual
+# map, the softmax from the first MFMA slot (`sm_mfma` 1) or also beside the
+# last item's first MFMA (`sm_late`), within 0.5% of the product's start.
 # Options of one map only, over PRODUCT[D]: the 12-wave D = 64 loop starts
 # its softmax one MFMA slot earlier and reads the row sum 8 wait states after
 # its MFMA (the compiler's own count for a 16x16x32 result read by VALU).  The
