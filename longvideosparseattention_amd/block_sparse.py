@@ -87,7 +87,8 @@ class BlockSparseAttentionWrapper:
 
     def _plan_for(self, head_dim: int, dtype: Optional[torch.dtype]) -> hip_ops.BlockPlan:
         # one block plan per tile height: fp32 runs 128-row tiles
-        block_q = hip_ops.attn_block_q(head_dim, dtype, self._plan_args["R"], self._plan_args["Cf"])
+        block_q = hip_ops.attn_block_q(head_dim, dtype, self._plan_args["R"], self._plan_args["Cf"],
+                                       n_k=self._plan_args["n_k"])
         plan = self._plans.get(block_q)
         if plan is None:
             plan = hip_ops.plan_build(self._bitmap, block_q=block_q, **self._plan_args)

@@ -109,18 +109,20 @@ class Layout:
     map: 64 rows per wave in two 32-row halves (NR = 2), the compact map's
     slots and temporaries, at most 256 VGPRs (two waves per SIMD)."""
 
-    def __init__(self, D: int, nw: int = 8, rs: bool = False):
-        assert (D, nw) in ((64, 8), (96, 8), (128, 8), (64, 12), (192, 4), (256, 4), (64, 4))
+    def __init__(self, D: int, nw: int = 8, rs: bool = False, dual: bool | None = None):
+        dual = (nw == 4 and D == 64) if dual is None else dual
+        assert (D, nw, dual) in ((64, 8, False), (96, 8, False), (128, 8, False), (64, 12, False), (192, 4, False),
+                                 (256, 4, False), (64, 4, True), (192, 4, True))
         self.D = D
         self.nw = nw
         self.wide = nw == 4 and D >= 192
-        self.dual = nw == 4 and D == 64   # two 32-row halves per wave (64 rows), two waves per SIMD
+        self.dual = dual                  # two 32-row halves per wave (64 rows)
         self.NR = 2 if self.dual else 1   # 32-row halves per wave
         assert rs or not self.dual
         self.rs = rs                      # row sums by MFMA: ONES (A pattern) and RS (result) tiles
-        compact = nw == 12 or self.dual
+        compact = nw == 12 or (self.dual and not self.wide)
         self.nslot = 4 if compact else NSLOT
-        self.NT = 8 if compact else 16    # softmax temporaries
+        self.NT = 8 if compact or self.dual else 16   # softmax temporaries
         self.NQK = D // 16                # MFMA k-steps of a score tile
         self.NDT = D // 32                # 32-wide d-tiles of O
         # D = 96 rows sit on the D = 128 LDS pitch and D = 192 rows on the
@@ -141,7 +143,13 @@ class Layout:
             return r - n
         NR = self.NR
         self.O = 0 if self.wide else take(16 * self.NDT * NR)   # wide: a[0 : 16 NDT]; dual: half 0, half 1
-        self.Q = take(4 * self.NQK * NR)
+        if self.wide and self.dual:
+            # the dual-wide map: Q of half 0 in VGPRs, of half 1 in the AGPRs after O
+            self.Q = take(4 * self.NQK)
+            self.QA = 16 * self.NDT * NR
+        else:
+            self.Q = take(4 * self.NQK * NR)
+            self.QA = None
         self.SA, self.SB = take(16 * NR), take(16 * NR)      # dual: the S tile of half r at + 16 r
         self.PA, self.PB = take(8 * NR), take(8 * NR)        # and its P at + 8 r
         self.OPS = take(4 * self.nslot)
@@ -166,9 +174,10 @@ class Layout:
             self.T = take(self.NT)
             self.RT = self.T                 # the rare path runs between softmaxes
         else:
-            self.RT = take(4)
-            self.T = take(16)
+            self.RT = take(4)                # (the wide maps scale O through T in the rare path)
+            self.T = take(self.NT)
         self.NVGPR = r
+        self.NAGPR = (16 * self.NDT * NR + (4 * self.NQK if self.QA is not None else 0)) if self.wide else 0
         sums = list(range(self.RS, self.RS + 4 * NR)) if rs else [self.LS0, self.LS1]
         self.CLOBBER_V = (list(range(self.SA, self.KOFF)) + sums + list(range(self.DK, self.DV + npar)) +
                           ([self.ROW1] if self.dual else []) + list(range(min(self.RT, self.T), self.NVGPR)))
@@ -197,10 +206,11 @@ class Gen:
                  and_scc: bool = False, copy_split: bool = False, sm_start: int = 2, rs_mfma: bool = False,
                  wait_pair: bool = False, rs_mix: bool = False, tail_nop: int = 12, tail_split: bool = False,
                  mask_fast: bool = False, mfma_order: str = "alt", copy_every: int = 2, prio: int = 0,
-                 dual_copy: tuple = (4, 8), sm_mfma: int | None = None, sm_late: bool = False):
+                 dual_copy: tuple = (4, 8), sm_mfma: int | None = None, sm_late: bool = False,
+                 dual: bool | None = None):
         assert dt in ("bf16", "f16")
         self.dt = dt
-        self.L = Layout(D, nw, rs=rs_mfma)
+        self.L = Layout(D, nw, rs=rs_mfma, dual=dual)
         self.rs_mfma = rs_mfma          # row sums by two 16x16x32 MFMAs against a ones pattern, no v_dot2
         self.wait_pair = wait_pair      # one LDS wait per two MFMAs (before the even one, for both)
         self.rs_mix = rs_mix            # rs_mfma softmax with the exponentials interleaved one by one
@@ -233,6 +243,14 @@ class Gen:
     def ov(self, a: int, n: int = 1) -> str:
         """O registers: AGPRs in the wide map, VGPRs otherwise."""
         return ar(a, n) if self.L.wide else vr(a, n)
+
+    def qreg(self, h: int, c: int) -> str:
+        """Q operand of k-step c for 32-row half h (the dual-wide map keeps half
+        1's Q in AGPRs)."""
+        L = self.L
+        if h == 1 and L.QA is not None:
+            return ar(L.QA + 4 * c, 4)
+        return vr(L.Q + 4 * L.NQK * h + 4 * c, 4)
 
     @property
     def mfma(self) -> str:
@@ -698,7 +716,7 @@ class Gen:
                 if m[0] == "qk":
                     _, _, _, c, S = m
                     S += 16 * h
-                    q = vr(L.Q + 4 * L.NQK * h + 4 * c, 4)
+                    q = self.qreg(h, c)
                     self.e(f"{self.mfma} {vr(S, 16)}, {vr(slot, 4)}, {q}, {'0' if c == 0 else vr(S, 16)}")
                 else:
                     _, _, st16, dt, P = m
@@ -773,7 +791,7 @@ class Gen:
             fill = {0: self.decode_wide(S_ENT + 2 * ((stage + 1) & 3), site, False) +
                     self.decode_wide(S_ENT + 2 * stage, site, True)}
             for k in range(2 * L.NCP):
-                self.place_copy(fill, 1 + self.copy_every * k, (stage + 1) & 1 if k < L.NCP else stage & 1, k)
+                self.place_copy(fill, self.u(1 + self.copy_every * k), (stage + 1) & 1 if k < L.NCP else stage & 1, k)
         else:
             fill = {0: self.decode(S_ENT + 2 * cst, site)}
             # copies after MFMAs spread over the block's 4*NQK*NR MFMAs
@@ -810,7 +828,7 @@ class Gen:
             fill = {0: self.decode_wide(S_ENT + 2, "F", False) + self.decode_wide(S_ENT, "F", True)}
             n = len(mf)
             for k in range(2 * L.NCP):
-                self.place_copy(fill, 1 + (k * (n - 2)) // (2 * L.NCP - 1), 1 if k < L.NCP else 0, k)
+                self.place_copy(fill, self.u(1 + (k * (n - 2)) // (2 * L.NCP - 1)), 1 if k < L.NCP else 0, k)
         else:
             fill = {0: self.decode(S_ENT + 4, "F")}
             for k in range(2 * L.NCP):
@@ -885,23 +903,41 @@ class Gen:
         return self.lines
 
 
-MAPS = ((128, 8), (96, 8), (64, 8), (64, 12), (64, 4), (256, 4), (192, 4))   # (head size, waves)
+# (head size, waves, two 32-row halves per wave): the dual map of D = 64 and
+# the dual-wide map of D = 192 run 64 rows per wave
+MAPS = ((128, 8, False), (96, 8, False), (64, 8, False), (64, 12, False), (64, 4, True), (256, 4, False),
+        (192, 4, False), (192, 4, True))
 
 
-def prefix(D: int, nw: int) -> str:
-    return f"LVSA_STREAM{D}" + ("" if nw == 8 else f"W{nw}")
+def map_key(D: int, nw: int, dual: bool) -> tuple:
+    """PRODUCT_MAP / per-map option key: (D, nw), or (D, nw, "dual") for the
+    dual-wide map (the one (D, nw) pair with two maps)."""
+    return (D, nw, "dual") if dual and D >= 192 else (D, nw)
 
 
-def operands(D: int, nw: int = 8, rs: bool = False) -> list[str]:
+def map_opts(D: int, nw: int, dual: bool) -> dict:
+    """The product's generator options for a map."""
+    return {**PRODUCT[D], **PRODUCT_MAP.get(map_key(D, nw, dual), {}), "dual": dual}
+
+
+def prefix(D: int, nw: int, dual: bool = False) -> str:
+    return f"LVSA_STREAM{D}" + ("" if nw == 8 else f"W{nw}") + ("D" if dual and D >= 192 else "")
+
+
+def operands(D: int, nw: int = 8, rs: bool = False, dual: bool | None = None) -> list[str]:
     """Macros with the asm operand lists of the D kernel (outputs, inputs, clobbers)."""
-    L = Layout(D, nw, rs)
-    pf = prefix(D, nw)
+    L = Layout(D, nw, rs, dual)
+    pf = prefix(D, nw, L.dual)
     no = L.NDT * L.NR                   # O tiles (dual: half 0's, then half 1's)
     os_ = ", ".join(f"o{t}" for t in range(no))
     orr = ar if L.wide else vr          # the wide map keeps O in AGPRs
     outs = ", ".join(f'"+{{{orr(L.O + 16 * t, 16)}}}"(o{t})' for t in range(no))
     outs += f', "+{{{vr(L.VM, 2 * L.NR)}}}"(ml), "+{{{vr(L.ROW, 4)}}}"(misc)'
-    if L.dual:                          # Q of both halves: one 32-register operand
+    if L.QA is not None:                # dual-wide: Q of half 0 in VGPRs, of half 1 in AGPRs, each 32 + 16
+        n = 4 * L.NQK
+        q = (f'"{{{vr(L.Q, 32)}}}"(qv.lo), "{{{vr(L.Q + 32, n - 32)}}}"(qv.hi), '
+             f'"{{{ar(L.QA, 32)}}}"(qv.alo), "{{{ar(L.QA + 32, n - 32)}}}"(qv.ahi)')
+    elif L.dual:                        # Q of both halves: one 32-register operand
         q = f'"{{{vr(L.Q, 4 * L.NQK * L.NR)}}}"(qv)'
     elif 4 * L.NQK in (24, 48, 64):   # no such operand class (or too wide): Q as two operands (qv.lo, qv.hi)
         lo = 16 if 4 * L.NQK == 24 else 32
@@ -975,7 +1011,8 @@ PRODUCT = {128: dict(lead=2, early_load=True, dot_init=True, and_scc=True, copy_
 # fewer cycles, 8 wait states 0.75%, copies 0.8%; together 6.0% fewer cycles
 # and 2.5% less time, the clock falling with the busier matrix core).
 PRODUCT_MAP = {(64, 12): dict(sm_start=1, tail_nop=8),
-               (64, 4): dict(sm_start=1, tail_nop=8, dual_copy=(6, 8))}
+               (64, 4): dict(sm_start=1, tail_nop=8, dual_copy=(6, 8)),
+               (192, 4, "dual"): {}}
 
 
 def render(per_d: dict | None = None, **opts) -> str:
@@ -983,11 +1020,11 @@ def render(per_d: dict | None = None, **opts) -> str:
            "// attn_fwd_stream_kernel (lvsa_attn_stream.h) and their asm operand lists.",
            "// Do not edit; regenerate.",
            "#pragma once", ""]
-    for D, nw in MAPS:
-        pf = prefix(D, nw)
+    for D, nw, dual in MAPS:
+        pf = prefix(D, nw, dual)
         for dt, name in (("bf16", f"{pf}_LOOP_BF16"), ("f16", f"{pf}_LOOP_F16")):
-            o = {**PRODUCT[D], **PRODUCT_MAP.get((D, nw), {}), **opts, **(per_d or {}).get(D, {}),
-                 **(per_d or {}).get((D, nw), {})}
+            o = {**map_opts(D, nw, dual), **opts, **(per_d or {}).get(D, {}),
+                 **(per_d or {}).get(map_key(D, nw, dual), {})}
             lines = Gen(dt, D=D, nw=nw, **o).build()
             out.append(f"#define {name} \\")
             for ln in lines:
@@ -998,7 +1035,7 @@ def render(per_d: dict | None = None, **opts) -> str:
                 out.append(f'  "{ln}\\n" \\')
             out.append('  ""')
             out.append("")
-        out += operands(D, nw, o.get("rs_mfma", False))
+        out += operands(D, nw, o.get("rs_mfma", False), dual)
         out.append("")
     return "\n".join(out)
 
@@ -1007,12 +1044,12 @@ CENSUS_KINDS = ("mfma 32x32x16", "mfma 16x16x32", "valu", "of which v_exp", "lds
                 "smem", "branch", "barrier", "s_waitcnt", "s_nop states")
 
 
-def census(D: int, nw: int, dt: str = "bf16") -> dict:
+def census(D: int, nw: int, dual: bool = False, dt: str = "bf16") -> dict:
     """Instruction counts per 32-key sub-block of the steady-state loop (the
     four unrolled blocks between LOOP and its back branch) of the product's
     loop for (D, nw): the common path, without the subroutines a masked
     block or the rare case calls."""
-    lines = Gen(dt, D=D, nw=nw, **{**PRODUCT[D], **PRODUCT_MAP.get((D, nw), {})}).build()
+    lines = Gen(dt, D=D, nw=nw, **map_opts(D, nw, dual)).build()
     a = next(i for i, x in enumerate(lines) if x.startswith("LOOP_"))
     b = next(i for i, x in enumerate(lines) if x.startswith("s_branch LOOP_"))
     c = dict.fromkeys(CENSUS_KINDS, 0)
@@ -1049,10 +1086,11 @@ def census(D: int, nw: int, dt: str = "bf16") -> dict:
 
 
 def print_census() -> None:
-    cols = [(128, 8), (96, 8), (64, 12), (64, 8), (64, 4), (192, 4), (256, 4)]
+    cols = [(128, 8, False), (96, 8, False), (64, 12, False), (64, 8, False), (64, 4, True), (192, 4, False),
+            (192, 4, True), (256, 4, False)]
     res = {col: census(*col) for col in cols}
     print("| per 32-key sub-block, per wave | " +
-          " | ".join(f"D={d}, {n} waves" + (" (64 rows)" if (d, n) == (64, 4) else "") for d, n in cols) + " |")
+          " | ".join(f"D={d}, {n} waves" + (" (64 rows)" if dual else "") for d, n, dual in cols) + " |")
     print("|---|" + "---|" * len(cols))
     for k in CENSUS_KINDS:
         print(f"| {k} | " + " | ".join(f"{res[col][k]:g}" for col in cols) + " |")

@@ -207,8 +207,9 @@ extern "C" int lvsa_attn_fwd(const lvsa_attn_args* a, hipStream_t stream) {
   LVSA_REQUIRE(a != nullptr, LVSA_ERR_INVALID_ARG, "lvsa_attn_fwd: null args");
   LVSA_REQUIRE(a->D == 64 || a->D == 96 || a->D == 128 || a->D == 192 || a->D == 256, LVSA_ERR_UNSUPPORTED,
                "lvsa_attn_fwd: head_dim %d not supported (64, 96, 128, 192, 256)", a->D);
-  LVSA_REQUIRE(a->D < 192 || a->block_q == kBM, LVSA_ERR_UNSUPPORTED,
-               "lvsa_attn_fwd: head_dim %d runs 128-row tiles (block_q %d)", a->D, a->block_q);
+  LVSA_REQUIRE(a->D < 192 || a->block_q == kBM || (a->D == 192 && a->block_q == kPPBM), LVSA_ERR_UNSUPPORTED,
+               "lvsa_attn_fwd: head_dim %d runs 128-row tiles (192 also 256-row ones; block_q %d)", a->D,
+               a->block_q);
   LVSA_REQUIRE(a->dtype == LVSA_BF16 || a->dtype == LVSA_FP16 || a->dtype == LVSA_FP32, LVSA_ERR_UNSUPPORTED,
                "lvsa_attn_fwd: dtype %d", a->dtype);
   const bool fp32 = a->dtype == LVSA_FP32;
@@ -363,6 +364,16 @@ extern "C" int lvsa_attn_fwd(const lvsa_attn_args* a, hipStream_t stream) {
   if (!fp32 && (a->D == 192 || a->D == 256) && a->block_q == kBM && !force_pp && stream_src &&
       (a->n_q == 0 || (p.R >= 127 && p.C >= 64)))
     p.use_stream = 1;
+  // D = 192 on 256-row tiles: the loop's dual-wide map, the only kernel for
+  // them (frames of >= 255 query rows).
+  if (a->D == 192 && a->block_q == kPPBM) {
+    LVSA_REQUIRE(!force_pp && stream_src && (a->n_q == 0 || (p.R >= 255 && p.C >= 64)), LVSA_ERR_UNSUPPORTED,
+                 "lvsa_attn_fwd: head_dim 192 on 256-row tiles needs frames of >= 255 query and >= 64 key rows, "
+                 "key sources below 2^31 bytes with row strides below 16 MiB, the last key block of the frame "
+                 "source inside one frame, and no LVSA_ATTN_KERNEL=pp (R %d, C %d); build the plan with block_q 128",
+                 p.R, p.C);
+    p.use_stream = 1;
+  }
   if (a->block_q == kStream12BM) {
     LVSA_REQUIRE(src32, LVSA_ERR_UNSUPPORTED,
                  "lvsa_attn_fwd: 384-row tiles address each key source with 32-bit byte offsets (source too large); "

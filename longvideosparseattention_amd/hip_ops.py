@@ -50,25 +50,36 @@ def attn_block_q(head_dim: int = 128, dtype: Optional[torch.dtype] = None, frame
     256 for head sizes 64, 96 and 128 in 16-bit: the single-stream kernels
     (head size 64: the dual map, 4 waves of 64 rows, two work-groups per CU)
     when query frames span at least 255 rows and key frames at least 64, the
-    8-wave ping-pong kernel otherwise.  128 for 192 and 256: the
-    single-stream kernel's wide map (4 waves, one per SIMD, when query frames
-    span at least 127 rows and key frames at least 64) or else the 4-wave
-    kernel, and for fp32 inputs at every head size (the fp32 kernel).
+    8-wave ping-pong kernel otherwise.  256 for 192 in 16-bit where the
+    single-stream kernel's dual-wide map (4 waves of 64 rows) takes the
+    geometry: query frames of at least 255 rows (``frame_rows``), key frames
+    of at least 64 (``key_rows``), and a key source of ``n_k`` rows from
+    token ``k_tok0`` whose short last block lies in one frame.  128 for 192
+    otherwise and for 256: the single-stream kernel's wide map (4 waves, one
+    per SIMD, when query frames span at least 127 rows and key frames at
+    least 64) or else the 4-wave kernel; and 128 for fp32 inputs at every
+    head size (the fp32 kernel).
 
     ``LVSA_ATTN_BLOCK_Q`` (128, 256 or 384) overrides the choice for 64 and
-    128 in 16-bit, for comparisons.  384 selects the 12-wave single-stream
-    kernel (head size 64, three waves of 32 rows per SIMD) where the geometry
-    allows it: query frames of at least 383 rows (``frame_rows``), key frames
-    of at least 64 (``key_rows``), and a key source of ``n_k`` rows from token
-    ``k_tok0`` whose short last block lies in one frame; 256 otherwise."""
+    128 in 16-bit, and 128 that for 192, for comparisons; so does
+    ``LVSA_ATTN_KERNEL=pp`` for 192 (the 4-wave kernel's 128-row tiles).
+    384 selects the 12-wave single-stream kernel (head size 64, three waves
+    of 32 rows per SIMD) where the geometry allows it (query frames of at
+    least 383 rows, the key conditions above); 256 otherwise."""
     kd = kernel_head_dim(head_dim)
     if dtype == torch.float32:
         return 128
+    env = os.environ.get("LVSA_ATTN_BLOCK_Q")
+    if kd == 192:
+        if env == "128" or os.environ.get("LVSA_ATTN_KERNEL") == "pp":
+            return 128
+        ok = (frame_rows >= 255 and key_rows >= capi.ATTN_BLOCK_K and
+              not stream_tail_crosses_frame(1, n_k, k_tok0, key_rows))
+        return 256 if ok else 128
     if kd >= 192:
         return 128
     if kd == 96:
         return 256
-    env = os.environ.get("LVSA_ATTN_BLOCK_Q")
     if env == "384":
         ok = (kd == 64 and frame_rows >= 383 and key_rows >= capi.ATTN_BLOCK_K and
               not stream_tail_crosses_frame(1, n_k, k_tok0, key_rows))
@@ -78,18 +89,33 @@ def attn_block_q(head_dim: int = 128, dtype: Optional[torch.dtype] = None, frame
     return 256
 
 
-def stream12_sources_ok(*srcs: Optional[torch.Tensor]) -> bool:
-    """Whether the 12-wave kernel (384-row tiles) can address these key /
-    value sources: its copies use one buffer resource per source with 32-bit
-    byte offsets, and 24-bit lane offsets (row x row stride in bytes).  The C
-    entry point rejects a 384-row plan otherwise."""
+def stream12_sources_ok(*srcs: Optional[torch.Tensor], limit: int = 1 << 32) -> bool:
+    """Whether the single-stream kernel can address these key / value
+    sources: its copies use one buffer resource per source with 32-bit byte
+    offsets (sources below ``limit`` bytes: 2^32, or 2^31 at head size 192,
+    whose lanes of a row's unused chunks add 0x7FFF0000), and 24-bit lane
+    offsets (row x row stride in bytes).  The C entry point rejects a 384-row
+    plan, or a 256-row plan at head size 192, otherwise."""
     for t in srcs:
         if t is None or t.shape[1] == 0:
             continue
         row = t.stride(1) * t.element_size()
-        if (t.shape[1] + capi.ATTN_BLOCK_K) * row >= (1 << 32) or row >= (1 << 24):
+        if (t.shape[1] + capi.ATTN_BLOCK_K) * row >= limit or row >= (1 << 24):
             return False
     return True
+
+
+def dual_wide_ok(plan: "BlockPlan", *srcs: Optional[torch.Tensor]) -> bool:
+    """Whether a call at head size 192 can run ``plan``'s 256-row tiles (the
+    dual-wide map, the only kernel for them): frames of at least 255 query
+    and 64 key rows, the frame source's short last key block inside one
+    frame, addressable sources, and no ``LVSA_ATTN_KERNEL=pp``.  The C entry
+    point makes the same test."""
+    p = plan.params
+    geom = p.n_q == 0 or (p.R >= 255 and p.C >= capi.ATTN_BLOCK_K and
+                          not stream_tail_crosses_frame(p.n_q, p.n_k, p.k_tok0, p.C))
+    return (geom and os.environ.get("LVSA_ATTN_KERNEL") != "pp" and
+            stream12_sources_ok(*srcs, limit=1 << 31))
 
 
 def _stream(device: torch.device) -> int:
@@ -232,19 +258,21 @@ class BlockPlan:
     def block_k(self) -> int:
         return self.params.block_k
 
-    def with_block_q_256(self) -> "BlockPlan":
-        """The same relation planned for 256-row tiles (built once, on the
-        current stream): what a 384-row plan falls back to when a call's key
-        sources exceed the 12-wave kernel's addressing."""
-        if self.block_q == 256:
+    def with_smaller_tiles(self) -> "BlockPlan":
+        """The same relation planned for the next smaller tiles (built once, on
+        the current stream): 256 rows for a 384-row plan when a call's key
+        sources exceed the 12-wave kernel's addressing, 128 for a 256-row plan
+        at head size 192 when a call does not fit the dual-wide map."""
+        if self.block_q == 128:
             return self
+        smaller = 256 if self.block_q == 384 else 128
         dev = self.tile_indptr.device
         capturing = torch.cuda.is_current_stream_capturing()
         if self._fallback is None:
             p = self.params
             self._fallback = plan_build(
                 self.rel, n_q=p.n_q, n_k=p.n_k, n_x=p.n_x, n_tq=p.n_tq, R=p.R, Cf=p.C, q_tok0=p.q_tok0,
-                k_tok0=p.k_tok0, q_frame0=p.q_frame0, max_row_frames=self.max_row_frames, block_q=256,
+                k_tok0=p.k_tok0, q_frame0=p.q_frame0, max_row_frames=self.max_row_frames, block_q=smaller,
                 block_k=p.block_k, device=dev)
             if not capturing:
                 self._fallback_ready = torch.cuda.Event()
@@ -381,7 +409,9 @@ def attn_args(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, plan: BlockPlan
     else:
         qt = None
     if plan.block_q == 384 and not stream12_sources_ok(k, v, kx, vx):
-        plan = plan.with_block_q_256()
+        plan = plan.with_smaller_tiles()
+    elif plan.block_q == 256 and D == 192 and not dual_wide_ok(plan, k, v, kx, vx):
+        plan = plan.with_smaller_tiles()
     pp = plan.params
     if plan.block_k != capi.ATTN_BLOCK_K:
         raise ValueError(f"plan built with block_k={plan.block_k}; the attention kernels walk key blocks of "

@@ -476,7 +476,9 @@ class Sim:
     def __init__(self, dt='bf16', **opts):
         # the product's loop for the head size, with any options of the test on top
         D, nw = opts.get("D", 128), opts.get("nw", 8)
-        lines = G.Gen(dt, **{**G.PRODUCT[D], **G.PRODUCT_MAP.get((D, nw), {}), **opts}).build()
+        dual = opts.get("dual")
+        dual = (nw == 4 and D == 64) if dual is None else dual
+        lines = G.Gen(dt, **{**G.map_opts(D, nw, dual), **opts}).build()
         self.nw = opts.get("nw", 8)
         self.prog, self.labels = parse_program(lines)
         self.mem = Mem()

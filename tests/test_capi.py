@@ -120,9 +120,12 @@ def test_attn_rejects_bad_args_without_launching():
     a.D, a.block_q = 96, 128
     assert lib.lvsa_attn_fwd(C.byref(a), None) == -2
     assert b"head_dim 96 runs 256-row tiles" in lib.lvsa_last_error()
-    a.D, a.block_q = 192, 256
+    a.D, a.block_q = 256, 256
     assert lib.lvsa_attn_fwd(C.byref(a), None) == -2
-    assert b"head_dim 192 runs 128-row tiles" in lib.lvsa_last_error()
+    assert b"head_dim 256 runs 128-row tiles" in lib.lvsa_last_error()
+    a.D, a.block_q = 192, 384
+    assert lib.lvsa_attn_fwd(C.byref(a), None) == -2
+    assert b"head_dim 192 runs 128-row tiles (192 also 256-row" in lib.lvsa_last_error()
     a.tile_indptr = a.entries = 4096         # host checks only: nothing is launched
     a.D, a.block_q = 128, 384                # 384-row tiles: head size 64 only
     assert lib.lvsa_attn_fwd(C.byref(a), None) == -2
@@ -150,6 +153,20 @@ def _attn_args(n_q=1000, rel_rows=10, n_tq=0, n_k=1000):
         setattr(a, f, _capi._Str3(1 << 20, 256, 128))
     a.words, a.R, a.C, a.rel_rows = 1, 100, 100, rel_rows
     return a
+
+
+def test_attn_head_192_on_256_row_tiles_needs_the_dual_wide_geometry():
+    """Head size 192 on 256-row tiles runs the dual-wide map only: query frames
+    below 255 rows, or a short last key block that crosses a frame, are
+    rejected before anything is launched."""
+    lib = _capi.lib()
+    a = _attn_args(n_q=1000, rel_rows=10)
+    a.D = 192
+    assert lib.lvsa_attn_fwd(C.byref(a), None) == -2          # R = C = 100
+    assert b"build the plan with block_q 128" in lib.lvsa_last_error()
+    a.R, a.C, a.rel_rows, a.k_tok0 = 300, 300, 4, 220           # (220 + 1000) % 300 = 20 < 40 tail rows
+    assert lib.lvsa_attn_fwd(C.byref(a), None) == -2
+    assert b"build the plan with block_q 128" in lib.lvsa_last_error()
 
 
 def test_attn_rejects_query_rows_outside_relation():

@@ -142,13 +142,14 @@ def test_lazy_exports():
 
 def test_head_sizes_of_the_plugin():
     """The reference plugin's head sizes (backend.py:52-53) all map onto a kernel:
-    every size runs natively; 96 on 256-row tiles, 192 and 256 on 128-row
-    tiles."""
+    every size runs natively; 96 on 256-row tiles, 192 on 256-row tiles
+    where the dual-wide map takes the geometry and 128-row ones otherwise,
+    256 on 128-row tiles."""
     from longvideosparseattention_amd import hip_ops
 
     assert hip_ops.SUPPORTED_HEAD_DIMS == (64, 96, 128, 192, 256)
     assert [hip_ops.kernel_head_dim(d) for d in (64, 96, 128, 192, 256)] == [64, 96, 128, 192, 256]
-    assert hip_ops.attn_block_q(256) == 128 and hip_ops.attn_block_q(192) == 128
+    assert hip_ops.attn_block_q(256) == 128 and hip_ops.attn_block_q(192) == 128   # no geometry: 128
     assert hip_ops.attn_block_q(96) == 256
     # head size 64: 256-row tiles (the dual map); fp32: 128
     assert hip_ops.attn_block_q(64, torch.bfloat16, 1350, 1350) == 256
@@ -157,6 +158,60 @@ def test_head_sizes_of_the_plugin():
     assert hip_ops.attn_block_q(128, torch.bfloat16, 1560, 1560) == 256
     with pytest.raises(ValueError, match="head_dim 80"):
         hip_ops.kernel_head_dim(80)
+
+
+def test_block_q_head_192(monkeypatch):
+    """Head size 192 in 16-bit: 256-row tiles (the dual-wide map) for query
+    frames >= 255 rows, key frames >= 64 and a short last key block inside
+    one frame; 128-row tiles (the wide map or the 4-wave kernel) otherwise,
+    for fp32, and with LVSA_ATTN_BLOCK_Q=128 or LVSA_ATTN_KERNEL=pp."""
+    from longvideosparseattention_amd import hip_ops
+
+    monkeypatch.delenv("LVSA_ATTN_BLOCK_Q", raising=False)
+    monkeypatch.delenv("LVSA_ATTN_KERNEL", raising=False)
+    assert hip_ops.attn_block_q(192, torch.bfloat16, 1560, 1560) == 256
+    assert hip_ops.attn_block_q(192, torch.float16, 255, 64) == 256
+    assert hip_ops.attn_block_q(192, torch.bfloat16, 254, 1560) == 128
+    assert hip_ops.attn_block_q(192, torch.bfloat16, 1560, 63) == 128
+    assert hip_ops.attn_block_q(192, torch.float32, 1560, 1560) == 128
+    assert hip_ops.attn_block_q(192, torch.bfloat16, 385, 385, n_k=440, k_tok0=0) == 128
+    assert hip_ops.attn_block_q(192, torch.bfloat16, 385, 385, n_k=440, k_tok0=440) == 256
+    assert hip_ops.attn_block_q(256, torch.bfloat16, 1560, 1560) == 128
+    monkeypatch.setenv("LVSA_ATTN_BLOCK_Q", "128")
+    assert hip_ops.attn_block_q(192, torch.bfloat16, 1560, 1560) == 128
+    monkeypatch.delenv("LVSA_ATTN_BLOCK_Q")
+    monkeypatch.setenv("LVSA_ATTN_KERNEL", "pp")
+    assert hip_ops.attn_block_q(192, torch.bfloat16, 1560, 1560) == 128
+
+
+def test_dual_wide_ok_mirrors_the_entry_point(monkeypatch):
+    """hip_ops.dual_wide_ok (the call-time test that sends a 256-row plan at
+    head size 192 to its 128-row fallback) accepts what the C entry point
+    accepts: frames, the last key block, source sizes below 2^31 bytes."""
+    from longvideosparseattention_amd import _capi as capi
+    from longvideosparseattention_amd import hip_ops
+
+    monkeypatch.delenv("LVSA_ATTN_KERNEL", raising=False)
+
+    def plan(n_q, n_k, R, C, k_tok0=0):
+        p = capi.PlanParams(n_q=n_q, n_k=n_k, R=R, C=C, k_tok0=k_tok0, block_q=256, block_k=64)
+        return hip_ops.BlockPlan(tile_indptr=None, entries=None, status=None, n_tiles=0, n_video_tiles=0,
+                                 params=p, rel=None)
+
+    def src(rows, row_elems):
+        return torch.empty_strided((1, rows, 1, 192), (0, row_elems, 192, 1), dtype=torch.bfloat16, device="meta")
+
+    k = src(4680, 192)
+    assert hip_ops.dual_wide_ok(plan(4680, 4680, 1560, 1560), k, k, None, None)
+    assert not hip_ops.dual_wide_ok(plan(4680, 4680, 254, 1560), k, k, None, None)
+    assert not hip_ops.dual_wide_ok(plan(4680, 4680, 1560, 63), k, k, None, None)
+    assert not hip_ops.dual_wide_ok(plan(1000, 440, 385, 385), k, k, None, None)        # tail crosses a frame
+    assert hip_ops.dual_wide_ok(plan(0, 440, 0, 0), k, k, None, None)                   # text rows only
+    big = (1 << 31) // (192 * 2)
+    assert not hip_ops.dual_wide_ok(plan(4680, big, 1560, 1560), src(big - 63, 192), k, None, None)
+    assert hip_ops.dual_wide_ok(plan(4680, big, 1560, 1560), src(big - 65, 192), k, None, None)
+    monkeypatch.setenv("LVSA_ATTN_KERNEL", "pp")
+    assert not hip_ops.dual_wide_ok(plan(4680, 4680, 1560, 1560), k, k, None, None)
 
 
 def test_block_q_override_384(monkeypatch):

@@ -52,9 +52,10 @@ def run_loop(entries, nk, n_x, seed=0, dt="bf16", D=128, nw=8, **opts):
     """Run the generated loop for the `nw` waves of one work-group with the
     registers the C++ prologue of attn_fwd_stream_kernel sets up (the 12-wave
     kernel: 384 query rows, waves 8-11 repeat the copies of waves 0-3; the
-    dual map, D = 64 with 4 waves: 64 rows per wave as two 32-row halves)."""
+    dual map, D = 64 with 4 waves, and the dual-wide map, D = 192 with 4 waves
+    and dual=True: 64 rows per wave as two 32-row halves)."""
     rng = np.random.default_rng(seed)
-    L = A.G.Layout(D, nw, rs=opts.get("rs_mfma", A.G.PRODUCT[D].get("rs_mfma", False)))
+    L = A.G.Layout(D, nw, rs=opts.get("rs_mfma", A.G.PRODUCT[D].get("rs_mfma", False)), dual=opts.get("dual"))
     NR = L.NR
     R = 32 * NR * nw
     RB, NCH = L.RB, L.RB // 16            # LDS row pitch (D = 96: the D = 128 pitch), chunks per row
@@ -80,7 +81,10 @@ def run_loop(entries, nk, n_x, seed=0, dt="bf16", D=128, nw=8, **opts):
             for c in range(L.NQK):
                 for j in range(4):
                     d0 = 16 * c + 8 * h + 2 * j
-                    V[L.Q + 4 * L.NQK * r + 4 * c + j] = qbits[rows, d0] | (qbits[rows, d0 + 1] << 16)
+                    # the dual-wide map holds half 1's Q in AGPRs (register file index 256 +)
+                    dst = (256 + L.QA + 4 * c + j if r == 1 and L.QA is not None
+                           else L.Q + 4 * L.NQK * r + 4 * c + j)
+                    V[dst] = qbits[rows, d0] | (qbits[rows, d0 + 1] << 16)
         sw = np.array([_swz(x & 15, D) for x in i32])
         for c in range(L.NQK):
             V[L.KOFF + c] = i32 * RB + (((2 * c + h) ^ sw) << 4)
@@ -266,4 +270,23 @@ def test_wide_loop_source_switches_rare_path_and_fp16(D):
     err, lse_err, _ = run_loop([(j, 0) for j in range(3)], 192, 0, seed=3, D=D, nw=4, always_rare=True)
     assert err <= 4e-3 and lse_err <= 2e-3, (err, lse_err)
     err, lse_err, _ = run_loop([(j, _tail(150, j)) for j in range(3)], 150, 0, seed=4, dt="f16", D=D, nw=4)
+    assert err <= 2e-3 and lse_err <= 2e-3, (err, lse_err)
+
+
+@pytest.mark.parametrize("case", sorted(CASES))
+def test_wide_loop_dual(case):
+    """The dual-wide map of D = 192: 4 waves of 64 rows (two 32-row halves
+    sharing each K and V operand read from LDS), 256-row tiles, O of both
+    halves and half 1's Q in AGPRs; the wide map's copies and rings."""
+    make, nk, n_x = CASES[case]
+    err, lse_err, copies = run_loop(make(), nk, n_x, D=192, nw=4, dual=True)
+    assert err <= 4e-3 and lse_err <= 2e-3, (case, err, lse_err)
+    assert copies == 4 * 8 * (1 + 2 * len(make()))
+
+
+def test_wide_loop_dual_rare_path_and_fp16():
+    err, lse_err, _ = run_loop([(j, 0) for j in range(3)], 192, 0, seed=6, D=192, nw=4, dual=True, always_rare=True)
+    assert err <= 4e-3 and lse_err <= 2e-3, (err, lse_err)
+    err, lse_err, _ = run_loop([(j, _tail(150, j)) for j in range(3)], 150, 0, seed=7, dt="f16", D=192, nw=4,
+                               dual=True)
     assert err <= 2e-3 and lse_err <= 2e-3, (err, lse_err)
