@@ -567,9 +567,12 @@ ALL_FRAMES = [
     ("wan6x_w4_four_offsets", 121, 1560, 4, 8, (1, 2, 6, 7), 12, 128, 0),
     ("hv_all_offsets", 49, 1590, 2, 8, tuple(range(8)), 16, 128, 256),
     ("cog_all_offsets", 13, 1350, 1, 4, tuple(range(4)), 48, 64, 226),
-    # the plugin's other head sizes at the Wan 4x geometry (96: D = 128 LDS layout; 192, 256: wide map)
+    # the plugin's other head sizes at the Wan 4x geometry (96: D = 128 LDS layout; 192: dual-wide map,
+    # 256-row tiles; 256: wide map), and 192 with text rows (HunyuanVideo geometry), fp16 and GQA
     ("wan4x_d96_off6", 84, 1560, 2, 8, (6,), 12, 96, 0),
     ("wan4x_d192_off1", 84, 1560, 2, 8, (1,), 12, 192, 0),
+    ("hv_d192_off3", 49, 1590, 2, 8, (3,), 16, 192, 256),
+    ("wan4x_d192_f16_gqa3_off4", 84, 1560, 2, 8, (4,), 12, 192, 0, torch.float16, 4),
     ("wan4x_d256_off7", 84, 1560, 2, 8, (7,), 12, 256, 0),
     # fp16 inputs (the loops' f16 variants)
     ("wan4x_f16_off0", 84, 1560, 2, 8, (0,), 12, 128, 0, torch.float16),
@@ -715,6 +718,7 @@ QUEUED = [
     (13, 1350, 24, 24, 64, 226, 1),  # CogVideoX frame size and text length, half the heads
     (13, 1350, 16, 4, 64, 226, 2),   # the same, GQA (16 query heads over 4) and batch 2: split tiles of both
     (40, 1560, 12, 12, 128, 0, 1),   # Wan frame size, video only
+    (24, 1100, 8, 2, 192, 300, 1),   # head size 192 (the dual-wide map), GQA, split text chunks
 ]
 
 
