@@ -202,8 +202,12 @@ typedef struct lvsa_attn_args {
   float scale;              /* softmax scale (reference: 1/sqrt(D))             */
   int32_t dtype;            /* lvsa_dtype                                       */
   /* plan (built with block_q = 128, 256 or 384 query rows and block_k = 64;
-   * D = 192 and 256 and fp32 run 128-row tiles only, D = 96 256-row tiles
-   * only, 384-row tiles are for D = 64 in 16 bit) */
+   * D = 256 and fp32 run 128-row tiles only, D = 96 256-row tiles only,
+   * 384-row tiles are for D = 64 in 16 bit; D = 192 in 16 bit runs 128-row
+   * tiles, or 256-row ones on the dual-wide map for frames of >= 255 query
+   * and >= 64 key rows whose frame source's short last key block lies in one
+   * frame, from sources below 2^31 bytes: other 256-row calls at D = 192
+   * return LVSA_ERR_UNSUPPORTED) */
   int32_t block_q;
   const int32_t* tile_indptr;
   const uint32_t* entries;

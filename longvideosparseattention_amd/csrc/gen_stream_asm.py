@@ -74,6 +74,12 @@ Register map (VGPRs; the kernel's operands pin them), D = 128 (D = 64):
   rows, K and V in two-stage rings of their own: block j copies K(j+1) and V(j)
   and waits for all copies at the next barrier, K and V tracking their key
   sources separately (SWITCHK / SWITCHV).  218 (194) VGPRs.
+  D = 192 by default runs the dual-wide map (Layout nw = 4, dual = True): the
+  wide map's copies, rings and AGPR-held O with the dual map's two 32-row
+  halves per wave (256-row tiles): O of half r in a[96 r : 96 r + 95], Q of
+  half 0 in v[0:47] and of half 1 in the AGPRs after O, a[192:239] (MFMAs
+  take B from AGPRs), the S, P, m, l and row-sum registers per half as in the
+  dual map, sixteen softmax temps: 241 VGPRs and 240 AGPRs.
 SGPRs: s[20:21] entry pointer, s22 blocks, s23 scale*log2(e), s[24:31] K/V
 bases (video, extra), s32-35 row strides, s36-37 source lengths, s38 wave,
 s39 LDS copy base of the wave; s40-s95 scratch.
@@ -107,7 +113,9 @@ class Layout:
     D = 192 and 256: one wave per SIMD, O in AGPRs, K and V in two-stage LDS
     rings of their own (rows on the 512-byte pitch); at D = 64 it is the dual
     map: 64 rows per wave in two 32-row halves (NR = 2), the compact map's
-    slots and temporaries, at most 256 VGPRs (two waves per SIMD)."""
+    slots and temporaries, at most 256 VGPRs (two waves per SIMD).  `dual`
+    with D = 192 is the dual-wide map: the wide map with two 32-row halves
+    per wave, half 1's Q in the AGPRs after O (QA)."""
 
     def __init__(self, D: int, nw: int = 8, rs: bool = False, dual: bool | None = None):
         dual = (nw == 4 and D == 64) if dual is None else dual
