@@ -287,7 +287,7 @@ def main(argv=None) -> int:
         "" if args.head_dim is None or args.head_dim == CONFIGS[args.config][3] else f"_d{D}")
     traffic, traffic_src, traffic_note = profiled_traffic(tag)
     # every 16-bit head size runs the single-stream kernel on these geometries
-    # (D = 192 and 256 in its wide map); LVSA_ATTN_KERNEL=pp selects the
+    # (D = 192 in its dual-wide map, 256 in its wide map); LVSA_ATTN_KERNEL=pp selects the
     # ping-pong kernel (D <= 128) or the 4-wave kernel (D >= 192)
     kernel = "attn_fwd_stream_kernel"
     if os.environ.get("LVSA_ATTN_KERNEL") == "pp":
