@@ -156,7 +156,7 @@ def single_prefill_with_kv_cache(q: torch.Tensor, k: torch.Tensor, v: torch.Tens
     if causal:
         raise NotImplementedError("causal prefill is not part of the LVSA path")
     hip_ops._require_device(q, "q")
-    key = (q.device, q.shape[0], k.shape[0], hip_ops.attn_block_q(q.shape[-1], q.dtype))
+    key = (q.device, q.shape[0], k.shape[0], hip_ops.attn_block_q(q.shape[-1], q.dtype, video_rows=False))
     plan = _DENSE_PLANS.get(key)
     if plan is None:
         plan = hip_ops.plan_build(None, n_q=0, n_k=k.shape[0], n_tq=q.shape[0], head_dim=q.shape[-1],

@@ -44,7 +44,7 @@ def stream_tail_crosses_frame(n_q: int, n_k: int, k_tok0: int, key_rows: int) ->
 
 
 def attn_block_q(head_dim: int = 128, dtype: Optional[torch.dtype] = None, frame_rows: int = 0,
-                 key_rows: int = 0, n_k: int = 0, k_tok0: int = 0) -> int:
+                 key_rows: int = 0, n_k: int = 0, k_tok0: int = 0, video_rows: bool = True) -> int:
     """Query rows per attention tile, i.e. which kernel a plan is built for.
 
     256 for head sizes 64, 96 and 128 in 16-bit: the single-stream kernels
@@ -54,8 +54,10 @@ def attn_block_q(head_dim: int = 128, dtype: Optional[torch.dtype] = None, frame
     single-stream kernel's dual-wide map (4 waves of 64 rows) takes the
     geometry: query frames of at least 255 rows (``frame_rows``), key frames
     of at least 64 (``key_rows``), and a key source of ``n_k`` rows from
-    token ``k_tok0`` whose short last block lies in one frame.  128 for 192
-    otherwise and for 256: the single-stream kernel's wide map (4 waves, one
+    token ``k_tok0`` whose short last block lies in one frame, or for a plan
+    without video query rows (``video_rows=False``: dense calls, whose rows
+    are text-query tiles that touch no frame).  128 for 192 otherwise and
+    for 256: the single-stream kernel's wide map (4 waves, one
     per SIMD, when query frames span at least 127 rows and key frames at
     least 64) or else the 4-wave kernel; and 128 for fp32 inputs at every
     head size (the fp32 kernel).
@@ -73,8 +75,8 @@ def attn_block_q(head_dim: int = 128, dtype: Optional[torch.dtype] = None, frame
     if kd == 192:
         if env == "128" or os.environ.get("LVSA_ATTN_KERNEL") == "pp":
             return 128
-        ok = (frame_rows >= 255 and key_rows >= capi.ATTN_BLOCK_K and
-              not stream_tail_crosses_frame(1, n_k, k_tok0, key_rows))
+        ok = not video_rows or (frame_rows >= 255 and key_rows >= capi.ATTN_BLOCK_K and
+                                not stream_tail_crosses_frame(1, n_k, k_tok0, key_rows))
         return 256 if ok else 128
     if kd >= 192:
         return 128
@@ -309,7 +311,8 @@ def plan_build(rel: Optional[torch.Tensor], *, n_q: int, n_k: int, n_x: int = 0,
     """Refine a frame relation (bitmap rows x words, int32) to token blocks.
 
     ``block_q`` defaults to the tile height of the kernel that serves
-    ``head_dim`` and ``dtype`` (see :func:`attn_block_q`)."""
+    ``head_dim`` and ``dtype`` (see :func:`attn_block_q`; without frame
+    geometry, except for a plan without video query rows)."""
     if rel is not None:
         _require_device(rel, "relation bitmap")
         device = rel.device
@@ -318,7 +321,7 @@ def plan_build(rel: Optional[torch.Tensor], *, n_q: int, n_k: int, n_x: int = 0,
         raise RuntimeError("lvsa_plan_build runs on the GPU only")
     device = torch.device(device)
     if block_q is None:
-        block_q = attn_block_q(head_dim, dtype)
+        block_q = attn_block_q(head_dim, dtype, video_rows=n_q > 0)
     p = capi.PlanParams()
     p.n_q, p.n_k, p.n_x, p.n_tq = n_q, n_k, n_x, n_tq
     p.R, p.C = R, Cf

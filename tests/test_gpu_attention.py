@@ -300,11 +300,14 @@ def test_build_global_kv_exact(gpu):
     assert torch.equal(full, kb)
 
 
-def test_single_prefill_dense(gpu):
-    q, k, v = (x.to(gpu) for x in _draw([(1, 70, 4, 128), (1, 333, 2, 128), (1, 333, 2, 128)]))
+@pytest.mark.parametrize("D", [128, 64, 96, 192, 256])
+def test_single_prefill_dense(D, gpu):
+    """Dense prefill at every head size (head size 192: 256-row tiles on the
+    dual-wide map, which a dense plan takes whatever its length)."""
+    q, k, v = (x.to(gpu) for x in _draw([(1, 300, 4, D), (1, 333, 2, D), (1, 333, 2, D)]))
     o, lse = lv.single_prefill_with_kv_cache(q[0], k[0], v[0], causal=False, return_lse=True)
     ro, rl = oa.dense_attention(q.float(), k.float(), v.float())
-    _close(o.unsqueeze(0), ro, "single_prefill")
+    _close(o.unsqueeze(0), ro, f"single_prefill D={D}")
     torch.testing.assert_close(lse.cpu(), rl[0].transpose(0, 1).cpu() / math.log(2.0), atol=3e-2, rtol=0)
 
 
@@ -823,12 +826,13 @@ def test_head64_maps_agree(cfg, gpu, monkeypatch):
         _close(ot12[:1], rto, "384-row tiles, text rows")
 
 
-def test_single_prefill_long_keys_split(gpu):
+@pytest.mark.parametrize("D", [128, 192])
+def test_single_prefill_long_keys_split(D, gpu):
     """Dense prefill over more than 128 key blocks runs split (chunks + merge)."""
-    q, k, v = (x.to(gpu) for x in _draw([(1, 70, 4, 128), (1, 20000, 2, 128), (1, 20000, 2, 128)], seed=5))
+    q, k, v = (x.to(gpu) for x in _draw([(1, 70, 4, D), (1, 20000, 2, D), (1, 20000, 2, D)], seed=5))
     o, lse = lv.single_prefill_with_kv_cache(q[0], k[0], v[0], causal=False, return_lse=True)
     ro, rl = oa.dense_attention(q.float(), k.float(), v.float())
-    _close(o.unsqueeze(0), ro, "single_prefill split")
+    _close(o.unsqueeze(0), ro, f"single_prefill split D={D}")
     torch.testing.assert_close(lse.cpu(), rl[0].transpose(0, 1).cpu() / math.log(2.0), atol=3e-2, rtol=0)
 
 

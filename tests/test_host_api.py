@@ -177,11 +177,16 @@ def test_block_q_head_192(monkeypatch):
     assert hip_ops.attn_block_q(192, torch.bfloat16, 385, 385, n_k=440, k_tok0=0) == 128
     assert hip_ops.attn_block_q(192, torch.bfloat16, 385, 385, n_k=440, k_tok0=440) == 256
     assert hip_ops.attn_block_q(256, torch.bfloat16, 1560, 1560) == 128
+    # no video query rows (dense calls): no frame condition
+    assert hip_ops.attn_block_q(192, torch.bfloat16, video_rows=False) == 256
+    assert hip_ops.attn_block_q(192, torch.float32, video_rows=False) == 128
+    assert hip_ops.attn_block_q(256, torch.bfloat16, video_rows=False) == 128
     monkeypatch.setenv("LVSA_ATTN_BLOCK_Q", "128")
     assert hip_ops.attn_block_q(192, torch.bfloat16, 1560, 1560) == 128
     monkeypatch.delenv("LVSA_ATTN_BLOCK_Q")
     monkeypatch.setenv("LVSA_ATTN_KERNEL", "pp")
     assert hip_ops.attn_block_q(192, torch.bfloat16, 1560, 1560) == 128
+    assert hip_ops.attn_block_q(192, torch.bfloat16, video_rows=False) == 128
 
 
 def test_dual_wide_ok_mirrors_the_entry_point(monkeypatch):

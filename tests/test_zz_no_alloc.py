@@ -38,7 +38,7 @@ def _noalloc(gpu, m, q, k, v, qt, kt, vt):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("D", [128, 64, 96, 256])
+@pytest.mark.parametrize("D", [128, 64, 96, 192, 256])
 def test_noalloc_matches_workspace_entry_point(D, gpu):
     # second call: smaller input.  Head size 64 takes 8 heads in the first
     # call: enough tiles for its two work-groups per CU to run the work queues
