@@ -1017,10 +1017,14 @@ PRODUCT = {128: dict(lead=2, early_load=True, dot_init=True, and_scc=True, copy_
 # dual map (D = 64, 4 waves of 64 rows) likewise, with its copies after MFMAs
 # 6, 14, 22 and 30 of a block (CogVideoX, against the defaults: start 1 5.6%
 # fewer cycles, 8 wait states 0.75%, copies 0.8%; together 6.0% fewer cycles
-# and 2.5% less time, the clock falling with the busier matrix core).
+# and 2.5% less time, the clock falling with the busier matrix core).  The
+# dual-wide map of D = 192 (key (192, 4, "dual")) runs PRODUCT[192] as it is:
+# against it at the Wan 4x geometry (three runs each, one box), lookahead 3, 5
+# or 6, the softmax from slot 3 or 8, no paired LDS waits, copies every MFMA
+# pair and 12 tail wait states all landed between -0.3% and +0.75%, and
+# copies every third MFMA pair +4.4%.
 PRODUCT_MAP = {(64, 12): dict(sm_start=1, tail_nop=8),
-               (64, 4): dict(sm_start=1, tail_nop=8, dual_copy=(6, 8)),
-               (192, 4, "dual"): {}}
+               (64, 4): dict(sm_start=1, tail_nop=8, dual_copy=(6, 8))}
 
 
 def render(per_d: dict | None = None, **opts) -> str:
