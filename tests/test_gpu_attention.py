@@ -721,7 +721,7 @@ QUEUED = [
     (13, 1350, 24, 24, 64, 226, 1),  # CogVideoX frame size and text length, half the heads
     (13, 1350, 16, 4, 64, 226, 2),   # the same, GQA (16 query heads over 4) and batch 2: split tiles of both
     (40, 1560, 12, 12, 128, 0, 1),   # Wan frame size, video only
-    (24, 1100, 8, 2, 192, 300, 1),   # head size 192 (the dual-wide map), GQA, split text chunks
+    (24, 1100, 8, 2, 192, 300, 2),   # head size 192 (the dual-wide map), GQA, split text chunks, batch 2
 ]
 
 
